@@ -1,0 +1,245 @@
+"""Throughput of bert_embed on one MI355X, in the driver's JSON-line format.
+
+Default workload: the synthetic varlen mix - 2000
+sentences, lognormal lengths clipped to [5, 64], consecutive batches of 64 in
+seeded order, each padded to round16(longest) (32 batches, eff 32/48/64).
+One step = one pass of bert_embed over all 32 pre-uploaded batches (the
+reference times passes over its corpus the same way, bench/corpus.cu:120-132).
+value = sentences/s over the K timed steps.
+
+The same line also carries, as extra fields: configs[1] (batch 64 x seq 16)
+and configs[2] (batch 64 x seq 128) sent/s (300 timed iterations as
+bench/bench.cu:32-51), configs[4] (batch 256 x seq 512) sent/s with the
+fused GEMMs' fraction of the fp16 dense MFMA peak, the roofline of the
+dominant kernel of the default workload (timed live with events on the stream
+the kernels run on), and the CPU baseline (the fp32 numpy oracle on a bounded
+sample, on this host's cores).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "bert-by-hand_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP16_DENSE = 2.5e15  # MI355X published dense fp16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12  # B/s
+
+# Algorithmic FLOPs of one Linear: 2*M*N*K.
+LAYER_GEMMS = [  # (name, N, K, epilogue)
+    ("qkv", 1152, 384, "bias"),
+    ("o_proj_ln", 384, 384, "ln"),
+    ("ffn1_gelu", 1536, 384, "gelu"),
+    ("ffn2_ln", 384, 1536, "ln"),
+]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(torch, fn, iters, warmup=3):
+    """Average ms per call of fn() between events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def gemm_runner(torch, engine, model_w, M, N, K, epi, buf):
+    """Closure launching one encoder GEMM at (M, N, K) with synthetic data."""
+    A = buf["A"][: M * K].view(M, K)
+    W = buf["W"][: N * K].view(N, K)
+    bias = buf["b"][:N]
+    C = buf["C"][: M * N].view(M, N)
+    if epi == "ln":
+        res = buf["R"][: M * 384].view(M, 384)
+        g, be = buf["g"], buf["be"]
+        return lambda: engine.launch_linear_residual_layernorm(A, W, bias, res, g, be, C, M, K)
+    return lambda: engine.launch_matmul(A, W, C, M, N, K, bias=bias, gelu=(epi == "gelu"))
+
+
+def gemm_buffers(torch, max_m):
+    g = torch.Generator(device="cuda").manual_seed(0)
+    mk = lambda n, s=1.0: (torch.randn(n, device="cuda", generator=g) * s).half()  # noqa: E731
+    return dict(A=mk(max_m * 1536), W=mk(1536 * 1536, 0.03), b=mk(1536, 0.02),
+                C=torch.empty(max_m * 1536, dtype=torch.float16, device="cuda"),
+                R=mk(max_m * 384), g=torch.ones(384, dtype=torch.float16, device="cuda"),
+                be=torch.zeros(384, dtype=torch.float16, device="cuda"))
+
+
+def cpu_baseline(batches, weights, budget_s=12.0):
+    """The fp32 numpy oracle (the reference's fp32 torch forward restated) on
+    the first batches of the same workload, until ~budget_s of CPU work."""
+    from oracle import bert_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    O.bert_embed(weights, *batches[0][:3])  # warm
+    n_sent, t0, used = 0, time.perf_counter(), 0
+    for ids, types, mask, _ in batches:
+        O.bert_embed(weights, ids, types, mask)
+        n_sent += ids.shape[0]
+        used += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n_sent / dt, 1), "unit": "sentences/s", "cores": int(cores),
+            "kind": "port",
+            "sample": f"fp32 numpy oracle bert_embed over the first {used} batches "
+                      f"({n_sent} sentences) of the varlen mix, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true", help="only the varlen workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only; the embedding path is pure data "
+              "parallel (whole batches per GPU, no collectives), so N>1 is not run.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from bbh import engine, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    weights = synth.make_weights(0)
+    model = engine.Model.from_weights(weights)
+    ws = engine.Workspace(256, 512)
+
+    # ---- default workload: varlen mix ------------------------------------
+    batches = synth.varlen_mix()
+    dev = [(torch.from_numpy(i).cuda(), torch.from_numpy(t).cuda(), torch.from_numpy(m).cuda(), s)
+           for i, t, m, s in batches]
+    n_sent = sum(b[0].shape[0] for b in batches)
+    emb = torch.empty((64, 384), dtype=torch.float16, device="cuda")
+
+    def step():
+        for i, t, m, _ in dev:
+            engine.bert_embed(ws, model, i, t, m, emb=emb[: i.shape[0]])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s_ev.record()
+    for _ in range(args.steps):
+        step()
+    e_ev.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = s_ev.elapsed_time(e_ev) / args.steps
+    sps = n_sent / (ms_step / 1e3)
+    total_flops = sum(synth.flops_per_forward(b[0].shape[0], b[3]) for b in batches)
+    log(f"varlen: {ms_step:.3f} ms/pass ({wall / args.steps * 1e3:.3f} ms wall), {sps:,.0f} sent/s, "
+        f"{total_flops / (ms_step / 1e3) / 1e12:.1f} TFLOP/s executed")
+
+    out = {
+        "metric": "sentences/sec (batch 64, seq 16/128 + varlen mix); % of MFMA fp16 peak",
+        "value": round(sps, 1), "unit": "sentences/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded random-init MiniLM-L6 weights N(0,0.02), synthetic token ids)",
+        "config": {"workload": "varlen mix: 2000 sentences, lognormal(median 12, sigma 0.5) "
+                               "lengths clipped to [5,64], consecutive batches of 64 padded to "
+                               "round16(max); one step = one pass over all 32 batches",
+                   "model": "MiniLM-L6 (6 layers, hidden 384, 12x32 heads, FFN 1536)",
+                   "global_batch": 64, "seq_len": "32/48/64 (mean eff 45.8)",
+                   "parallelism": "single GPU"},
+        "ms_per_sentence": round(ms_step / n_sent, 6),
+        "executed_tflops": round(total_flops / (ms_step / 1e3) / 1e12, 2),
+    }
+
+    # ---- dominant kernel of the default workload ---------------------------
+    buf = gemm_buffers(torch, 131072)
+    M_dom = 64 * 48  # the most common batch shape of the mix (21 of 32 batches)
+    per_kernel = {}
+    for name, N, K, epi in LAYER_GEMMS:
+        fn = gemm_runner(torch, engine, model, M_dom, N, K, epi, buf)
+        ms = timed(torch, fn, 200)
+        per_kernel[name] = {"ms": ms, "flops": 2.0 * M_dom * N * K}
+    qkv = torch.randn((M_dom, 1152), device="cuda").half()
+    msk = torch.ones((64, 48), dtype=torch.int32, device="cuda")
+    ctx = torch.empty((M_dom, 384), dtype=torch.float16, device="cuda")
+    ms_att = timed(torch, lambda: engine.launch_attention(qkv, msk, ctx, 64, 48), 200)
+    per_kernel["attention"] = {"ms": ms_att, "flops": 4.0 * 64 * 12 * 32 * 48 * 48}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
+    d = per_kernel[dom]
+    ach = d["flops"] / (d["ms"] / 1e3)
+    out["roofline"] = {"bound": "mfma", "kernel": dom, "shape": f"M={M_dom} (batch 64 x eff 48)",
+                       "achieved": round(ach / 1e12, 2), "peak": PEAK_FP16_DENSE / 1e12,
+                       "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_DENSE, 4), "traffic": None,
+                       "avg_launch_us": round(d["ms"] * 1e3, 2)}
+    out["per_kernel_us_at_eff48"] = {k: round(v["ms"] * 1e3, 2) for k, v in per_kernel.items()}
+    log("per-kernel us at M=3072:", out["per_kernel_us_at_eff48"])
+
+    if not args.no_extras:
+        # ---- batch 64 x seq 16 / 128 ----------------
+        for tag, seq in (("cfg2_b64_s16", 16), ("cfg3_b64_s128", 128)):
+            ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(64, seq))
+            ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb), 300,
+                       warmup=20)
+            out[tag] = {"sentences_per_s": round(64 / (ms / 1e3), 1),
+                        "ms_per_sentence": round(ms / 64, 6),
+                        "tflops": round(synth.flops_per_forward(64, seq) / (ms / 1e3) / 1e12, 2)}
+            log(tag, out[tag])
+        # ---- batch 256 x seq 512 ---------------------------------
+        ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())
+        emb5 = torch.empty((256, 384), dtype=torch.float16, device="cuda")
+        ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb5), 10,
+                   warmup=2)
+        gemm_ms, gemm_flops = 0.0, 0.0
+        gem = {}
+        for name, N, K, epi in LAYER_GEMMS:
+            fn = gemm_runner(torch, engine, model, 131072, N, K, epi, buf)
+            t = timed(torch, fn, 10, warmup=2)
+            f = 2.0 * 131072 * N * K
+            gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
+            gemm_ms += t
+            gemm_flops += f
+        out["cfg5_b256_s512"] = {
+            "sentences_per_s": round(256 / (ms / 1e3), 1), "ms_per_forward": round(ms, 3),
+            "tflops": round(synth.flops_per_forward(256, 512) / (ms / 1e3) / 1e12, 2),
+            "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
+            "per_gemm_frac": gem}
+        log("cfg5", out["cfg5_b256_s512"])
+
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(batches, weights)
+        log("cpu baseline", out["cpu_baseline"])
+    else:
+        out["cpu_baseline"] = None
+
+    ws.close()
+    model.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,265 @@
+"""Host-side mirror of the reference's C++ API over the C ABI, for torch
+device tensors (torch is used only for device memory and streams).
+
+Reference names kept: ``load_model_weights`` (src/model/weights.h:88),
+``make_workspace`` (src/model/workspace.h:20), ``bert_embed`` / ``bert_encode``
+(src/model/forward.h:11-19), ``encoder_layer`` / ``attention_block`` /
+``ffn_block`` (src/model/encoder.h:27-46) and the ``launch_*`` kernel
+launchers (src/kernels/*.h).  Like the reference, every call only enqueues
+work on the current stream; errors raise ``BBHError`` instead of aborting.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import capi
+from .capi import call, lib
+
+HIDDEN = 384
+NUM_LAYERS = 6
+NUM_HEADS = 12
+HEAD_DIM = 32
+FFN_DIM = 1536
+LAYER_NORM_EPS = 1e-12
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(stream=None):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    torch = _torch()
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Model:
+    """Device-resident weights (the reference's ModelWeights)."""
+
+    def __init__(self, handle: ctypes.c_void_p):
+        self.handle = handle
+
+    @classmethod
+    def from_weights(cls, weights: dict) -> "Model":
+        """weights: state_dict name -> array (any float dtype; cast to fp16 RNE)."""
+        L = lib()
+        n = L.bbh_param_count()
+        keep, ptrs = [], (ctypes.c_void_p * n)()
+        for i in range(n):
+            name = L.bbh_param_name(i).decode()
+            arr = np.ascontiguousarray(np.asarray(weights[name]).astype(np.float16))
+            if arr.size != L.bbh_param_numel(i):
+                raise ValueError(f"{name}: expected {L.bbh_param_numel(i)} elements, got {arr.size}")
+            keep.append(arr)
+            ptrs[i] = arr.ctypes.data
+        h = ctypes.c_void_p()
+        call("bbh_model_from_host", ptrs, n, ctypes.byref(h))
+        return cls(h)
+
+    @classmethod
+    def load_dir(cls, directory: str) -> "Model":
+        h = ctypes.c_void_p()
+        call("bbh_model_load_dir", directory.encode(), ctypes.byref(h))
+        return cls(h)
+
+    def close(self):
+        if self.handle:
+            call("bbh_model_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Workspace:
+    """All scratch of a forward, allocated once (the reference's Workspace)."""
+
+    def __init__(self, max_batch: int, max_seq: int = 128):
+        self.max_batch, self.max_seq = max_batch, max_seq
+        self.handle = ctypes.c_void_p()
+        call("bbh_workspace_create", max_batch, max_seq, ctypes.byref(self.handle))
+
+    def hidden(self, batch: int, seq: int):
+        """Zero-copy (batch*seq, 384) fp16 view of the final-hidden buffer
+        (ws.attn_out); holds the encoder output after bert_embed."""
+        torch = _torch()
+        if batch * seq > self.max_batch * self.max_seq:
+            raise ValueError("view larger than the workspace")
+        ptr = lib().bbh_workspace_hidden(self.handle)
+        return torch.as_tensor(_DeviceArray(ptr, (batch * seq, HIDDEN), "<f2"), device="cuda")
+
+    def close(self):
+        if self.handle:
+            call("bbh_workspace_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _DeviceArray:
+    """Minimal __cuda_array_interface__ exporter for a device pointer the
+    library owns (torch.as_tensor wraps it without copying)."""
+
+    def __init__(self, ptr: int, shape, typestr: str):
+        self.__cuda_array_interface__ = {"shape": tuple(shape), "typestr": typestr,
+                                         "data": (int(ptr), False), "version": 3,
+                                         "strides": None}
+
+
+def load_model_weights(weights_or_dir) -> Model:
+    if isinstance(weights_or_dir, (str, bytes)):
+        return Model.load_dir(weights_or_dir)
+    return Model.from_weights(weights_or_dir)
+
+
+def make_workspace(batch: int = 1, max_seq: int = 128) -> Workspace:
+    return Workspace(batch, max_seq)
+
+
+def _check_i32(*ts):
+    torch = _torch()
+    for t in ts:
+        if t.dtype != torch.int32 or not t.is_contiguous() or not t.is_cuda:
+            raise TypeError("ids/types/mask must be contiguous int32 CUDA tensors")
+
+
+def bert_embed(ws: Workspace, w: Model, ids, types, mask, emb=None, batch=None, seq=None,
+               stream=None):
+    """(batch, seq) int32 device tensors -> (batch, 384) fp16 embeddings."""
+    torch = _torch()
+    _check_i32(ids, types, mask)
+    batch = ids.shape[0] if batch is None else batch
+    seq = ids.shape[-1] if seq is None else seq
+    if emb is None:
+        emb = torch.empty((batch, HIDDEN), dtype=torch.float16, device=ids.device)
+    call("bbh_embed", ws.handle, w.handle, _ptr(ids), _ptr(types), _ptr(mask), _ptr(emb), batch, seq,
+         _stream(stream))
+    return emb
+
+
+def bert_encode(ws: Workspace, w: Model, ids, types, mask, out=None, batch=None, seq=None,
+                stream=None):
+    torch = _torch()
+    _check_i32(ids, types, mask)
+    batch = ids.shape[0] if batch is None else batch
+    seq = ids.shape[-1] if seq is None else seq
+    if out is None:
+        out = torch.empty((batch * seq, HIDDEN), dtype=torch.float16, device=ids.device)
+    call("bbh_encode", ws.handle, w.handle, _ptr(ids), _ptr(types), _ptr(mask), _ptr(out), batch,
+         seq, _stream(stream))
+    return out
+
+
+def attention_block(ws, w, layer, hidden, mask, out, batch, seq, stream=None):
+    call("bbh_attention_block", ws.handle, w.handle, layer, _ptr(hidden), _ptr(mask), _ptr(out),
+         batch, seq, _stream(stream))
+    return out
+
+
+def ffn_block(ws, w, layer, hidden, out, batch, seq, stream=None):
+    call("bbh_ffn_block", ws.handle, w.handle, layer, _ptr(hidden), _ptr(out), batch, seq,
+         _stream(stream))
+    return out
+
+
+def encoder_layer(ws, w, layer, hidden, mask, out, batch, seq, stream=None):
+    call("bbh_encoder_layer", ws.handle, w.handle, layer, _ptr(hidden), _ptr(mask), _ptr(out),
+         batch, seq, _stream(stream))
+    return out
+
+
+# ---- kernel launchers (src/kernels/*.h) ------------------------------------
+
+def launch_matmul(A, B, C, M, N, K, bias=None, gelu=False, stream=None):
+    call("bbh_linear", _ptr(A), _ptr(B), _ptr(C), M, N, K, _ptr(bias), int(bool(gelu)),
+         _stream(stream))
+    return C
+
+
+def launch_linear_residual_layernorm(A, B, bias, residual, gamma, beta, y, M, K,
+                                     eps=LAYER_NORM_EPS, stream=None):
+    call("bbh_linear_residual_layernorm", _ptr(A), _ptr(B), _ptr(bias), _ptr(residual),
+         _ptr(gamma), _ptr(beta), _ptr(y), M, HIDDEN, K, ctypes.c_float(eps), _stream(stream))
+    return y
+
+
+def launch_layernorm(x, gamma, beta, y, M, D, eps=LAYER_NORM_EPS, residual=None, stream=None):
+    call("bbh_layernorm", _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), M, D, ctypes.c_float(eps),
+         _ptr(residual), _stream(stream))
+    return y
+
+
+def launch_embedding(ids, types, word, pos, typ, out, seq, hidden, batch=1, stream=None):
+    call("bbh_embedding", _ptr(ids), _ptr(types), _ptr(word), _ptr(pos), _ptr(typ), _ptr(out), seq,
+         hidden, batch, _stream(stream))
+    return out
+
+
+def launch_embedding_layernorm(ids, types, word, pos, typ, gamma, beta, out, seq, batch=1,
+                               eps=LAYER_NORM_EPS, stream=None):
+    call("bbh_embedding_layernorm", _ptr(ids), _ptr(types), _ptr(word), _ptr(pos), _ptr(typ),
+         _ptr(gamma), _ptr(beta), _ptr(out), seq, HIDDEN, batch, ctypes.c_float(eps), _stream(stream))
+    return out
+
+
+def launch_attention(qkv, mask, merged, batch, seq, heads=NUM_HEADS, head_dim=HEAD_DIM,
+                     scale=None, stream=None):
+    scale = 1.0 / np.sqrt(head_dim) if scale is None else scale
+    call("bbh_attention", _ptr(qkv), _ptr(mask), _ptr(merged), batch, heads, seq, head_dim,
+         ctypes.c_float(scale), _stream(stream))
+    return merged
+
+
+def launch_attention_scores(qkv, scores, batch, heads, seq, head_dim, qkv_stride, q_off, k_off,
+                            scale, stream=None):
+    call("bbh_attention_scores", _ptr(qkv), _ptr(scores), batch, heads, seq, head_dim, qkv_stride,
+         q_off, k_off, ctypes.c_float(scale), _stream(stream))
+    return scores
+
+
+def launch_softmax(x, M, N, mask=None, mask_stride=0, stream=None):
+    call("bbh_softmax", _ptr(x), M, N, _ptr(mask), mask_stride, _stream(stream))
+    return x
+
+
+def launch_attention_context(probs, qkv, merged, batch, heads, seq, head_dim, qkv_stride, v_off,
+                             stream=None):
+    call("bbh_attention_context", _ptr(probs), _ptr(qkv), _ptr(merged), batch, heads, seq, head_dim,
+         qkv_stride, v_off, _stream(stream))
+    return merged
+
+
+def launch_mean_pool(hidden, mask, out, seq, dim, batch=1, stream=None):
+    call("bbh_mean_pool", _ptr(hidden), _ptr(mask), _ptr(out), seq, dim, batch, _stream(stream))
+    return out
+
+
+def launch_l2_normalize(x, n, batch=1, stream=None):
+    call("bbh_l2_normalize", _ptr(x), n, batch, _stream(stream))
+    return x
+
+
+def launch_pool_normalize(hidden, mask, out, seq, batch=1, stream=None):
+    call("bbh_pool_normalize", _ptr(hidden), _ptr(mask), _ptr(out), seq, HIDDEN, batch,
+         _stream(stream))
+    return out
+
+
+BBHError = capi.BBHError

@@ -1,0 +1,629 @@
+// C ABI of the engine (include/bbh.h): weight loading, workspace, forward
+// orchestration, argument validation and error reporting.
+//
+// Forward per encoder layer (the reference's attention_block + ffn_block,
+// src/model/encoder.cu:25-71, with 9 launches per layer) is 5 launches here:
+//   1. QKV GEMM + bias                       hidden   -> qkv      (M, 1152)
+//   2. fused masked attention                qkv      -> ctx      (M, 384)
+//   3. O GEMM + bias + residual(hidden) + LN ctx      -> attn_out (M, 384)
+//   4. FFN1 GEMM + bias + GELU               attn_out -> inter    (M, 1536)
+//   5. FFN2 GEMM + bias + residual + LN      inter    -> out      (M, 384)
+// plus one fused embedding+LN launch before the layers and one fused
+// pool+normalize launch after them: 32 launches per bert_embed against the
+// reference's 58 launches and a device-to-device copy (src/model/forward.cu).
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <math.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/bbh.h"
+#include "kernels.h"
+
+using bbh::f16;
+
+namespace {
+
+thread_local std::string g_err;
+
+bbh_status fail(bbh_status s, const std::string& msg) {
+  g_err = msg;
+  return s;
+}
+
+bbh_status hip_fail(hipError_t e, const char* what) {
+  return fail(BBH_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) + " (" +
+                               hipGetErrorString(e) + ")");
+}
+
+#define BBH_HIP(call, what)                           \
+  do {                                                \
+    hipError_t _e = (call);                           \
+    if (_e != hipSuccess) return hip_fail(_e, what);  \
+  } while (0)
+
+struct Param {
+  std::string name;
+  size_t numel;
+};
+
+const std::vector<Param>& params() {
+  static const std::vector<Param> p = [] {
+    std::vector<Param> v;
+    const size_t H = BBH_HIDDEN, F = BBH_FFN_DIM;
+    v.push_back({"embeddings.word_embeddings.weight", (size_t)BBH_VOCAB_SIZE * H});
+    v.push_back({"embeddings.position_embeddings.weight", (size_t)BBH_MAX_POSITION * H});
+    v.push_back({"embeddings.token_type_embeddings.weight", (size_t)BBH_TYPE_VOCAB_SIZE * H});
+    v.push_back({"embeddings.LayerNorm.weight", H});
+    v.push_back({"embeddings.LayerNorm.bias", H});
+    for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+      const std::string p = "encoder.layer." + std::to_string(i) + ".";
+      for (const char* part : {"query", "key", "value"}) {
+        v.push_back({p + "attention.self." + part + ".weight", H * H});
+        v.push_back({p + "attention.self." + part + ".bias", H});
+      }
+      v.push_back({p + "attention.output.dense.weight", H * H});
+      v.push_back({p + "attention.output.dense.bias", H});
+      v.push_back({p + "attention.output.LayerNorm.weight", H});
+      v.push_back({p + "attention.output.LayerNorm.bias", H});
+      v.push_back({p + "intermediate.dense.weight", F * H});
+      v.push_back({p + "intermediate.dense.bias", F});
+      v.push_back({p + "output.dense.weight", H * F});
+      v.push_back({p + "output.dense.bias", H});
+      v.push_back({p + "output.LayerNorm.weight", H});
+      v.push_back({p + "output.LayerNorm.bias", H});
+    }
+    return v;
+  }();
+  return p;
+}
+
+constexpr int kPerLayer = 16;  // state_dict tensors per encoder layer
+constexpr int kEmbParams = 5;
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct bbh_model {
+  void* blob = nullptr;
+  size_t bytes = 0;
+  const f16 *word, *pos, *type, *emb_g, *emb_b;
+  struct Layer {
+    const f16 *qkv_w, *qkv_b, *o_w, *o_b, *ln1_g, *ln1_b;
+    const f16 *f1_w, *f1_b, *f2_w, *f2_b, *ln2_g, *ln2_b;
+  } layers[BBH_NUM_LAYERS];
+};
+
+struct bbh_workspace {
+  int max_batch = 0, max_seq = 0;
+  size_t rows = 0;
+  void* blob = nullptr;
+  size_t bytes = 0;
+  f16 *qkv, *ctx, *attn_out, *inter, *ping, *pong;
+};
+
+namespace {
+
+// Device blob layout: the five embedding tensors, then per layer
+// qkv_w (1152x384, Q|K|V rows), qkv_b, o_w, o_b, ln1 g/b, f1_w, f1_b, f2_w,
+// f2_b, ln2 g/b; every array starts on a 256-byte boundary.
+struct BlobLayout {
+  std::vector<size_t> off;  // offset (elements) of each state_dict tensor in the blob
+  size_t total = 0;         // elements
+};
+
+const BlobLayout& layout() {
+  static const BlobLayout L = [] {
+    BlobLayout l;
+    const auto& p = params();
+    l.off.assign(p.size(), 0);
+    size_t cur = 0;  // bytes
+    auto put = [&](int idx) {
+      l.off[idx] = cur / sizeof(f16);
+      cur = align256(cur + p[idx].numel * sizeof(f16));
+    };
+    for (int i = 0; i < kEmbParams; ++i) put(i);
+    for (int L_ = 0; L_ < BBH_NUM_LAYERS; ++L_) {
+      const int b0 = kEmbParams + L_ * kPerLayer;
+      // Q|K|V weights contiguous (fused 1152x384), then Q|K|V biases contiguous.
+      const size_t H = BBH_HIDDEN;
+      l.off[b0 + 0] = cur / 2;
+      l.off[b0 + 2] = cur / 2 + H * H;
+      l.off[b0 + 4] = cur / 2 + 2 * H * H;
+      cur = align256(cur + 3 * H * H * 2);
+      l.off[b0 + 1] = cur / 2;
+      l.off[b0 + 3] = cur / 2 + H;
+      l.off[b0 + 5] = cur / 2 + 2 * H;
+      cur = align256(cur + 3 * H * 2);
+      for (int k = 6; k < kPerLayer; ++k) put(b0 + k);
+    }
+    l.total = cur / sizeof(f16);
+    return l;
+  }();
+  return L;
+}
+
+bbh_status model_from_host_blob(const std::vector<uint16_t>& host, bbh_model** out) {
+  const BlobLayout& L = layout();
+  bbh_model* m = new bbh_model();
+  m->bytes = L.total * sizeof(f16);
+  hipError_t e = hipMalloc(&m->blob, m->bytes);
+  if (e != hipSuccess) {
+    delete m;
+    return fail(BBH_ERR_OOM, std::string("hipMalloc(weights): ") + hipGetErrorString(e));
+  }
+  e = hipMemcpy(m->blob, host.data(), m->bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(m->blob);
+    delete m;
+    return hip_fail(e, "hipMemcpy(weights)");
+  }
+  const f16* base = static_cast<const f16*>(m->blob);
+  auto at = [&](int idx) { return base + L.off[idx]; };
+  m->word = at(0);
+  m->pos = at(1);
+  m->type = at(2);
+  m->emb_g = at(3);
+  m->emb_b = at(4);
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    const int b0 = kEmbParams + i * kPerLayer;
+    auto& l = m->layers[i];
+    l.qkv_w = at(b0 + 0);
+    l.qkv_b = at(b0 + 1);
+    l.o_w = at(b0 + 6);
+    l.o_b = at(b0 + 7);
+    l.ln1_g = at(b0 + 8);
+    l.ln1_b = at(b0 + 9);
+    l.f1_w = at(b0 + 10);
+    l.f1_b = at(b0 + 11);
+    l.f2_w = at(b0 + 12);
+    l.f2_b = at(b0 + 13);
+    l.ln2_g = at(b0 + 14);
+    l.ln2_b = at(b0 + 15);
+  }
+  *out = m;
+  return BBH_OK;
+}
+
+hipStream_t S(bbh_stream_t s) { return static_cast<hipStream_t>(s); }
+
+bbh_status check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return hip_fail(e, what);
+  return BBH_OK;
+}
+
+#define BBH_TRY(expr)                    \
+  do {                                   \
+    bbh_status _s = (expr);              \
+    if (_s != BBH_OK) return _s;         \
+  } while (0)
+
+bbh_status check_shape(const bbh_workspace* ws, int batch, int seq) {
+  if (batch < 1 || seq < 1)
+    return fail(BBH_ERR_INVALID_ARG,
+                "batch and seq must be positive (batch=" + std::to_string(batch) +
+                    ", seq=" + std::to_string(seq) + ")");
+  if (seq % BBH_SEQ_ALIGN != 0)
+    return fail(BBH_ERR_SEQ_ALIGN, "seq must be a multiple of 16 (seq=" + std::to_string(seq) + ")");
+  if (seq > BBH_MAX_POSITION)
+    return fail(BBH_ERR_CAPACITY, "seq " + std::to_string(seq) + " exceeds max position 512");
+  if (ws) {
+    if (seq > ws->max_seq)
+      return fail(BBH_ERR_CAPACITY, "seq " + std::to_string(seq) + " exceeds workspace max_seq " +
+                                        std::to_string(ws->max_seq));
+    if ((size_t)batch * seq > ws->rows)
+      return fail(BBH_ERR_CAPACITY,
+                  "batch*seq " + std::to_string((size_t)batch * seq) +
+                      " exceeds workspace capacity " + std::to_string(ws->rows) + " rows");
+  }
+  return BBH_OK;
+}
+
+bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
+
+bbh_status misaligned(const char* what) {
+  return fail(BBH_ERR_INVALID_ARG, std::string(what) + ": device pointer not aligned for vector access");
+}
+
+const float kScale = 0.17677669529663687f;  // 1 / sqrt(32), src/model/encoder.cu:28
+
+bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                               const int32_t* mask, f16* out, int batch, int seq,
+                               hipStream_t s) {
+  const int M = batch * seq;
+  BBH_TRY(check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * BBH_HIDDEN,
+                                 BBH_HIDDEN, bbh::Act::kNone, s),
+                       "qkv gemm"));
+  BBH_TRY(check_launch(bbh::attention(ws->qkv, mask, ws->ctx, batch, BBH_NUM_HEADS, seq,
+                                      kScale, s),
+                       "attention"));
+  BBH_TRY(check_launch(bbh::gemm_residual_ln(ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g, L.ln1_b,
+                                             out, M, BBH_HIDDEN, BBH_LAYER_NORM_EPS, s),
+                       "o-proj gemm+ln"));
+  return BBH_OK;
+}
+
+bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                         f16* out, int batch, int seq, hipStream_t s) {
+  const int M = batch * seq;
+  BBH_TRY(check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, BBH_FFN_DIM, BBH_HIDDEN,
+                                 bbh::Act::kGelu, s),
+                       "ffn1 gemm"));
+  BBH_TRY(check_launch(bbh::gemm_residual_ln(ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
+                                             L.ln2_b, out, M, BBH_FFN_DIM, BBH_LAYER_NORM_EPS,
+                                             s),
+                       "ffn2 gemm+ln"));
+  return BBH_OK;
+}
+
+// Embeddings + 6 layers; the last layer writes `final_out` (which may be
+// ws->attn_out: the FFN2+LN epilogue reads each residual element before the
+// same thread overwrites it).
+bbh_status run_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                      const int32_t* types, const int32_t* mask, f16* final_out, int batch,
+                      int seq, hipStream_t s) {
+  BBH_TRY(check_launch(bbh::embedding_ln(ids, types, m->word, m->pos, m->type, m->emb_g,
+                                         m->emb_b, ws->ping, batch, seq, BBH_LAYER_NORM_EPS, s),
+                       "embedding+ln"));
+  f16* cur = ws->ping;
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
+    BBH_TRY(run_attention_block(ws, m->layers[i], cur, mask, ws->attn_out, batch, seq, s));
+    BBH_TRY(run_ffn_block(ws, m->layers[i], ws->attn_out, nxt, batch, seq, s));
+    cur = nxt;
+  }
+  return BBH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bbh_status_string(bbh_status s) {
+  switch (s) {
+    case BBH_OK: return "ok";
+    case BBH_ERR_INVALID_ARG: return "invalid argument";
+    case BBH_ERR_SEQ_ALIGN: return "seq not a multiple of 16";
+    case BBH_ERR_CAPACITY: return "capacity exceeded";
+    case BBH_ERR_IO: return "weight file error";
+    case BBH_ERR_HIP: return "HIP runtime error";
+    case BBH_ERR_OOM: return "device out of memory";
+    case BBH_ERR_UNSUPPORTED: return "unsupported shape";
+  }
+  return "unknown status";
+}
+
+const char* bbh_last_error(void) { return g_err.c_str(); }
+
+const char* bbh_version(void) { return "bbh 0.1 gfx950"; }
+
+int bbh_param_count(void) { return (int)params().size(); }
+
+const char* bbh_param_name(int index) {
+  if (index < 0 || index >= (int)params().size()) return nullptr;
+  return params()[index].name.c_str();
+}
+
+size_t bbh_param_numel(int index) {
+  if (index < 0 || index >= (int)params().size()) return 0;
+  return params()[index].numel;
+}
+
+bbh_status bbh_model_from_host(const uint16_t* const* tensors, int n_tensors, bbh_model** out) {
+  if (!tensors || !out) return fail(BBH_ERR_INVALID_ARG, "null tensors/out");
+  if (n_tensors != bbh_param_count())
+    return fail(BBH_ERR_INVALID_ARG, "expected " + std::to_string(bbh_param_count()) +
+                                         " tensors, got " + std::to_string(n_tensors));
+  const auto& p = params();
+  const BlobLayout& L = layout();
+  std::vector<uint16_t> host(L.total, 0);
+  for (int i = 0; i < n_tensors; ++i) {
+    if (!tensors[i]) return fail(BBH_ERR_INVALID_ARG, "null tensor " + p[i].name);
+    memcpy(host.data() + L.off[i], tensors[i], p[i].numel * sizeof(uint16_t));
+  }
+  return model_from_host_blob(host, out);
+}
+
+bbh_status bbh_model_load_dir(const char* dir, bbh_model** out) {
+  if (!dir || !out) return fail(BBH_ERR_INVALID_ARG, "null dir/out");
+  const auto& p = params();
+  const BlobLayout& L = layout();
+  std::vector<uint16_t> host(L.total, 0);
+  for (size_t i = 0; i < p.size(); ++i) {
+    const std::string path = std::string(dir) + "/" + p[i].name + ".bin";
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return fail(BBH_ERR_IO, "cannot open " + path);
+    fseek(f, 0, SEEK_END);
+    const long sz = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    const size_t want = p[i].numel * sizeof(uint16_t);
+    if (sz < 0 || (size_t)sz != want) {
+      fclose(f);
+      return fail(BBH_ERR_IO, path + ": expected " + std::to_string(want) + " bytes, found " +
+                                  std::to_string(sz));
+    }
+    const size_t got = fread(host.data() + L.off[i], sizeof(uint16_t), p[i].numel, f);
+    fclose(f);
+    if (got != p[i].numel)
+      return fail(BBH_ERR_IO, path + ": short read (" + std::to_string(got) + " of " +
+                                  std::to_string(p[i].numel) + " elements)");
+  }
+  return model_from_host_blob(host, out);
+}
+
+bbh_status bbh_model_free(bbh_model* m) {
+  if (!m) return BBH_OK;
+  hipError_t e = m->blob ? hipFree(m->blob) : hipSuccess;
+  delete m;
+  if (e != hipSuccess) return hip_fail(e, "hipFree(weights)");
+  return BBH_OK;
+}
+
+size_t bbh_model_device_bytes(const bbh_model* m) { return m ? m->bytes : 0; }
+
+size_t bbh_workspace_bytes(int max_batch, int max_seq) {
+  if (max_batch < 1 || max_seq < 1) return 0;
+  const size_t rows = (size_t)max_batch * max_seq;
+  const size_t H = BBH_HIDDEN;
+  return align256(rows * 3 * H * 2) + align256(rows * BBH_FFN_DIM * 2) + 4 * align256(rows * H * 2);
+}
+
+bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out) {
+  if (!out) return fail(BBH_ERR_INVALID_ARG, "null out");
+  if (max_batch < 1 || max_seq < 1)
+    return fail(BBH_ERR_INVALID_ARG, "max_batch and max_seq must be positive");
+  if (max_seq % BBH_SEQ_ALIGN != 0)
+    return fail(BBH_ERR_SEQ_ALIGN, "max_seq must be a multiple of 16");
+  if (max_seq > BBH_MAX_POSITION)
+    return fail(BBH_ERR_CAPACITY, "max_seq exceeds max position 512");
+  bbh_workspace* ws = new bbh_workspace();
+  ws->max_batch = max_batch;
+  ws->max_seq = max_seq;
+  ws->rows = (size_t)max_batch * max_seq;
+  ws->bytes = bbh_workspace_bytes(max_batch, max_seq);
+  hipError_t e = hipMalloc(&ws->blob, ws->bytes);
+  if (e != hipSuccess) {
+    delete ws;
+    return fail(BBH_ERR_OOM, std::string("hipMalloc(workspace): ") + hipGetErrorString(e));
+  }
+  char* p = static_cast<char*>(ws->blob);
+  const size_t H = BBH_HIDDEN, rows = ws->rows;
+  auto take = [&](size_t bytes) {
+    f16* r = reinterpret_cast<f16*>(p);
+    p += align256(bytes);
+    return r;
+  };
+  ws->qkv = take(rows * 3 * H * 2);
+  ws->inter = take(rows * BBH_FFN_DIM * 2);
+  ws->ctx = take(rows * H * 2);
+  ws->attn_out = take(rows * H * 2);
+  ws->ping = take(rows * H * 2);
+  ws->pong = take(rows * H * 2);
+  *out = ws;
+  return BBH_OK;
+}
+
+bbh_status bbh_workspace_free(bbh_workspace* ws) {
+  if (!ws) return BBH_OK;
+  hipError_t e = ws->blob ? hipFree(ws->blob) : hipSuccess;
+  delete ws;
+  if (e != hipSuccess) return hip_fail(e, "hipFree(workspace)");
+  return BBH_OK;
+}
+
+void* bbh_workspace_hidden(bbh_workspace* ws) { return ws ? ws->attn_out : nullptr; }
+
+bbh_status bbh_embed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                     const int32_t* types, const int32_t* mask, void* emb, int batch, int seq,
+                     bbh_stream_t stream) {
+  if (!ws || !m || !ids || !types || !mask || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed: null argument");
+  BBH_TRY(check_shape(ws, batch, seq));
+  const hipStream_t s = S(stream);
+  BBH_TRY(run_encode(ws, m, ids, types, mask, ws->attn_out, batch, seq, s));
+  return check_launch(bbh::pool_normalize(ws->attn_out, mask, static_cast<f16*>(emb), batch, seq, s),
+                      "pool+normalize");
+}
+
+bbh_status bbh_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                      const int32_t* types, const int32_t* mask, void* out, int batch, int seq,
+                      bbh_stream_t stream) {
+  if (!ws || !m || !ids || !types || !mask || !out)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_encode: null argument");
+  BBH_TRY(check_shape(ws, batch, seq));
+  return run_encode(ws, m, ids, types, mask, static_cast<f16*>(out), batch, seq, S(stream));
+}
+
+static bbh_status check_layer(const bbh_workspace* ws, const bbh_model* m, int layer,
+                              const void* hidden, const void* out, int batch, int seq) {
+  if (!ws || !m || !hidden || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (layer < 0 || layer >= BBH_NUM_LAYERS)
+    return fail(BBH_ERR_INVALID_ARG, "layer index " + std::to_string(layer) + " out of range");
+  if (hidden == out) return fail(BBH_ERR_INVALID_ARG, "out may not alias hidden");
+  return check_shape(ws, batch, seq);
+}
+
+bbh_status bbh_attention_block(bbh_workspace* ws, const bbh_model* m, int layer,
+                               const void* hidden, const int32_t* mask, void* out, int batch,
+                               int seq, bbh_stream_t stream) {
+  BBH_TRY(check_layer(ws, m, layer, hidden, out, batch, seq));
+  if (!mask) return fail(BBH_ERR_INVALID_ARG, "null mask");
+  return run_attention_block(ws, m->layers[layer], static_cast<const f16*>(hidden), mask,
+                             static_cast<f16*>(out), batch, seq, S(stream));
+}
+
+bbh_status bbh_ffn_block(bbh_workspace* ws, const bbh_model* m, int layer, const void* hidden,
+                         void* out, int batch, int seq, bbh_stream_t stream) {
+  BBH_TRY(check_layer(ws, m, layer, hidden, out, batch, seq));
+  return run_ffn_block(ws, m->layers[layer], static_cast<const f16*>(hidden),
+                       static_cast<f16*>(out), batch, seq, S(stream));
+}
+
+bbh_status bbh_encoder_layer(bbh_workspace* ws, const bbh_model* m, int layer,
+                             const void* hidden, const int32_t* mask, void* out, int batch,
+                             int seq, bbh_stream_t stream) {
+  BBH_TRY(check_layer(ws, m, layer, hidden, out, batch, seq));
+  if (!mask) return fail(BBH_ERR_INVALID_ARG, "null mask");
+  if (out == ws->attn_out) return fail(BBH_ERR_INVALID_ARG, "out may not be the workspace's attn_out");
+  const hipStream_t s = S(stream);
+  BBH_TRY(run_attention_block(ws, m->layers[layer], static_cast<const f16*>(hidden), mask,
+                              ws->attn_out, batch, seq, s));
+  return run_ffn_block(ws, m->layers[layer], ws->attn_out, static_cast<f16*>(out), batch, seq, s);
+}
+
+bbh_status bbh_linear(const void* A, const void* B, void* C, int M, int N, int K,
+                      const void* bias, int gelu, bbh_stream_t stream) {
+  if (!A || !B || !C) return fail(BBH_ERR_INVALID_ARG, "bbh_linear: null operand");
+  if (M < 1 || N < 1 || K < 1) return fail(BBH_ERR_INVALID_ARG, "bbh_linear: M, N, K must be positive");
+  return check_launch(bbh::gemm(static_cast<const f16*>(A), static_cast<const f16*>(B),
+                                static_cast<const f16*>(bias), static_cast<f16*>(C), M, N, K,
+                                gelu ? bbh::Act::kGelu : bbh::Act::kNone, S(stream)),
+                      "linear");
+}
+
+bbh_status bbh_linear_residual_layernorm(const void* A, const void* B, const void* bias,
+                                         const void* residual, const void* gamma,
+                                         const void* beta, void* y, int M, int N, int K,
+                                         float eps, bbh_stream_t stream) {
+  if (!A || !B || !bias || !residual || !gamma || !beta || !y)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_linear_residual_layernorm: null argument");
+  if (M < 1 || K < 1) return fail(BBH_ERR_INVALID_ARG, "M and K must be positive");
+  if (N != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "N must be 384");
+  if (K % 32 != 0) return fail(BBH_ERR_UNSUPPORTED, "K must be a multiple of 32");
+  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(bias, 8) || !aligned(residual, 8) ||
+      !aligned(gamma, 8) || !aligned(beta, 8) || !aligned(y, 8))
+    return misaligned("bbh_linear_residual_layernorm");
+  return check_launch(
+      bbh::gemm_residual_ln(static_cast<const f16*>(A), static_cast<const f16*>(B),
+                            static_cast<const f16*>(bias), static_cast<const f16*>(residual),
+                            static_cast<const f16*>(gamma), static_cast<const f16*>(beta),
+                            static_cast<f16*>(y), M, K, eps, S(stream)),
+      "linear+residual+layernorm");
+}
+
+bbh_status bbh_layernorm(const void* x, const void* gamma, const void* beta, void* y, int M,
+                         int D, float eps, const void* residual, bbh_stream_t stream) {
+  if (!x || !gamma || !beta || !y) return fail(BBH_ERR_INVALID_ARG, "bbh_layernorm: null argument");
+  if (M < 1 || D < 1 || D > 4096) return fail(BBH_ERR_INVALID_ARG, "bbh_layernorm: bad M/D");
+  return check_launch(bbh::layernorm(static_cast<const f16*>(x), static_cast<const f16*>(residual),
+                                     static_cast<const f16*>(gamma), static_cast<const f16*>(beta),
+                                     static_cast<f16*>(y), M, D, eps, S(stream)),
+                      "layernorm");
+}
+
+bbh_status bbh_embedding(const int32_t* ids, const int32_t* types, const void* word,
+                         const void* pos, const void* type, void* out, int seq, int hidden,
+                         int batch, bbh_stream_t stream) {
+  if (!ids || !types || !word || !pos || !type || !out)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embedding: null argument");
+  if (seq < 1 || hidden < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (seq > BBH_MAX_POSITION) return fail(BBH_ERR_CAPACITY, "seq exceeds max position 512");
+  return check_launch(bbh::embedding(ids, types, static_cast<const f16*>(word),
+                                     static_cast<const f16*>(pos), static_cast<const f16*>(type),
+                                     static_cast<f16*>(out), batch, seq, hidden, S(stream)),
+                      "embedding");
+}
+
+bbh_status bbh_embedding_layernorm(const int32_t* ids, const int32_t* types, const void* word,
+                                   const void* pos, const void* type, const void* gamma,
+                                   const void* beta, void* out, int seq, int hidden, int batch,
+                                   float eps, bbh_stream_t stream) {
+  if (!ids || !types || !word || !pos || !type || !gamma || !beta || !out)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embedding_layernorm: null argument");
+  if (hidden != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "hidden must be 384");
+  if (seq < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (seq > BBH_MAX_POSITION) return fail(BBH_ERR_CAPACITY, "seq exceeds max position 512");
+  if (!aligned(word, 4) || !aligned(pos, 4) || !aligned(type, 4) || !aligned(gamma, 4) ||
+      !aligned(beta, 4) || !aligned(out, 4))
+    return misaligned("bbh_embedding_layernorm");
+  return check_launch(bbh::embedding_ln(ids, types, static_cast<const f16*>(word),
+                                        static_cast<const f16*>(pos), static_cast<const f16*>(type),
+                                        static_cast<const f16*>(gamma), static_cast<const f16*>(beta),
+                                        static_cast<f16*>(out), batch, seq, eps, S(stream)),
+                      "embedding+layernorm");
+}
+
+bbh_status bbh_attention(const void* qkv, const int32_t* mask, void* merged, int batch, int heads,
+                         int seq, int head_dim, float scale, bbh_stream_t stream) {
+  if (!qkv || !mask || !merged) return fail(BBH_ERR_INVALID_ARG, "bbh_attention: null argument");
+  if (batch < 1 || heads < 1 || seq < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (head_dim != BBH_HEAD_DIM) return fail(BBH_ERR_UNSUPPORTED, "head_dim must be 32");
+  if (seq % BBH_SEQ_ALIGN) return fail(BBH_ERR_SEQ_ALIGN, "seq must be a multiple of 16");
+  if (seq > BBH_MAX_POSITION) return fail(BBH_ERR_CAPACITY, "seq exceeds 512");
+  if (!aligned(qkv, 16) || !aligned(merged, 8)) return misaligned("bbh_attention");
+  return check_launch(bbh::attention(static_cast<const f16*>(qkv), mask, static_cast<f16*>(merged),
+                                     batch, heads, seq, scale, S(stream)),
+                      "attention");
+}
+
+bbh_status bbh_attention_scores(const void* qkv, void* scores, int batch, int heads, int seq,
+                                int head_dim, int qkv_stride, int q_off, int k_off, float scale,
+                                bbh_stream_t stream) {
+  if (!qkv || !scores) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (batch < 1 || heads < 1 || seq < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (head_dim != BBH_HEAD_DIM) return fail(BBH_ERR_UNSUPPORTED, "head_dim must be 32");
+  if (seq % BBH_SEQ_ALIGN) return fail(BBH_ERR_SEQ_ALIGN, "seq must be a multiple of 16");
+  if (qkv_stride % 8 || q_off % 8 || k_off % 8 || q_off < 0 || k_off < 0 ||
+      q_off + heads * head_dim > qkv_stride || k_off + heads * head_dim > qkv_stride)
+    return fail(BBH_ERR_INVALID_ARG, "qkv_stride/q_off/k_off must be multiples of 8 inside the row");
+  if (!aligned(qkv, 16)) return misaligned("bbh_attention_scores");
+  return check_launch(bbh::attention_scores(static_cast<const f16*>(qkv), static_cast<f16*>(scores),
+                                            batch, heads, seq, qkv_stride, q_off, k_off, scale,
+                                            S(stream)),
+                      "attention_scores");
+}
+
+bbh_status bbh_softmax(void* x, int M, int N, const int32_t* mask, int mask_stride,
+                       bbh_stream_t stream) {
+  if (!x) return fail(BBH_ERR_INVALID_ARG, "null x");
+  if (M < 1 || N < 1 || mask_stride < 0) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  return check_launch(bbh::softmax_rows(static_cast<f16*>(x), M, N, mask, mask_stride, S(stream)),
+                      "softmax");
+}
+
+bbh_status bbh_attention_context(const void* probs, const void* qkv, void* merged, int batch,
+                                 int heads, int seq, int head_dim, int qkv_stride, int v_off,
+                                 bbh_stream_t stream) {
+  if (!probs || !qkv || !merged) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (batch < 1 || heads < 1 || seq < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (head_dim != BBH_HEAD_DIM) return fail(BBH_ERR_UNSUPPORTED, "head_dim must be 32");
+  if (v_off < 0 || v_off + heads * head_dim > qkv_stride)
+    return fail(BBH_ERR_INVALID_ARG, "v_off outside the qkv row");
+  return check_launch(bbh::attention_context(static_cast<const f16*>(probs),
+                                             static_cast<const f16*>(qkv), static_cast<f16*>(merged),
+                                             batch, heads, seq, qkv_stride, v_off, S(stream)),
+                      "attention_context");
+}
+
+bbh_status bbh_mean_pool(const void* hidden, const int32_t* mask, void* out, int seq, int dim,
+                         int batch, bbh_stream_t stream) {
+  if (!hidden || !mask || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (seq < 1 || dim < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  return check_launch(bbh::mean_pool(static_cast<const f16*>(hidden), mask, static_cast<f16*>(out),
+                                     batch, seq, dim, S(stream)),
+                      "mean_pool");
+}
+
+bbh_status bbh_l2_normalize(void* x, int n, int batch, bbh_stream_t stream) {
+  if (!x) return fail(BBH_ERR_INVALID_ARG, "null x");
+  if (n < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  return check_launch(bbh::l2_normalize(static_cast<f16*>(x), n, batch, S(stream)), "l2_normalize");
+}
+
+bbh_status bbh_pool_normalize(const void* hidden, const int32_t* mask, void* out, int seq, int dim,
+                              int batch, bbh_stream_t stream) {
+  if (!hidden || !mask || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (dim != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "dim must be 384");
+  if (seq < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (!aligned(hidden, 4) || !aligned(out, 4)) return misaligned("bbh_pool_normalize");
+  return check_launch(bbh::pool_normalize(static_cast<const f16*>(hidden), mask,
+                                          static_cast<f16*>(out), batch, seq, S(stream)),
+                      "pool+normalize");
+}
+
+}  // extern "C"

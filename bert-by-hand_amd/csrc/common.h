@@ -1,0 +1,66 @@
+// Device-side helpers shared by the gfx950 kernels of the embedding engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bbh {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kHidden = 384;
+constexpr int kHeads = 12;
+constexpr int kHeadDim = 32;
+constexpr int kFfn = 1536;
+constexpr int kVocab = 30522;
+constexpr int kMaxPos = 512;
+constexpr int kTypes = 2;
+
+// Sum / max over the 64 lanes of a wavefront (butterfly, every lane gets it).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Reduction over the four 16-lane groups that share lane % 16 (the lanes that
+// hold one row / column of a 16x16 MFMA tile).
+__device__ inline float group4_sum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+__device__ inline float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+// Exact GELU, x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), with the device
+// library's erff (src/kernels/matmul.cu:27-28 uses the same definition).
+__device__ inline float gelu_erf(float v) {
+  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+// D(16x16, fp32) += A(16x32, fp16) . B(32x16, fp16) on the CDNA4 matrix core.
+// Lane l supplies row (l % 16) of A and column (l % 16) of B, each as 8
+// consecutive k values of k-group (l / 16); it receives D rows
+// 4*(l/16) .. 4*(l/16)+3 of column (l % 16).
+__device__ inline f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace bbh

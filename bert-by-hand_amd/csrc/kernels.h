@@ -1,0 +1,60 @@
+// Host launchers of the gfx950 kernels.  Each enqueues on `s` and returns the
+// launch status; argument validation happens in capi.cpp before these run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace bbh {
+
+enum class Act { kNone, kGelu };
+
+// C(M,N) = A(M,K) . W(N,K)^T [+ bias] [GELU].  True when the MFMA path takes
+// the shape (N % 64 == 0, K % 64 == 0); otherwise the plain tiled kernel runs.
+bool gemm_mfma_ok(int N, int K);
+hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N,
+                int K, Act act, hipStream_t s);
+
+// y(M,384) = LN(A(M,K) . W(384,K)^T + bias + residual) * gamma + beta.
+// y may alias residual.  K % 64 == 0.
+hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
+                            const f16* residual, const f16* gamma, const f16* beta,
+                            f16* y, int M, int K, float eps, hipStream_t s);
+
+// Fused masked attention from the QKV activations (row stride 3*heads*32).
+hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
+                     int heads, int seq, float scale, hipStream_t s);
+
+// Reference-shaped attention pieces (unfused): scores, masked softmax, context.
+hipError_t attention_scores(const f16* qkv, f16* scores, int batch, int heads, int seq,
+                            int qkv_stride, int q_off, int k_off, float scale,
+                            hipStream_t s);
+hipError_t softmax_rows(f16* x, int M, int N, const int32_t* mask, int mask_stride,
+                        hipStream_t s);
+hipError_t attention_context(const f16* probs, const f16* qkv, f16* merged, int batch,
+                             int heads, int seq, int qkv_stride, int v_off,
+                             hipStream_t s);
+
+// Row LayerNorm of (x [+ residual]); y may alias x or residual.
+hipError_t layernorm(const f16* x, const f16* residual, const f16* gamma,
+                     const f16* beta, f16* y, int M, int D, float eps, hipStream_t s);
+
+// Embedding gather-sum, plain and fused with the embedding LayerNorm.
+hipError_t embedding(const int32_t* ids, const int32_t* types, const f16* word,
+                     const f16* pos, const f16* type, f16* out, int batch, int seq,
+                     int hidden, hipStream_t s);
+hipError_t embedding_ln(const int32_t* ids, const int32_t* types, const f16* word,
+                        const f16* pos, const f16* type, const f16* gamma,
+                        const f16* beta, f16* out, int batch, int seq, float eps,
+                        hipStream_t s);
+
+// Masked mean pool, L2 normalise, and the two fused.
+hipError_t mean_pool(const f16* hidden, const int32_t* mask, f16* out, int batch,
+                     int seq, int dim, hipStream_t s);
+hipError_t l2_normalize(f16* x, int n, int batch, hipStream_t s);
+hipError_t pool_normalize(const f16* hidden, const int32_t* mask, f16* out, int batch,
+                          int seq, hipStream_t s);
+
+}  // namespace bbh

@@ -1,0 +1,287 @@
+// Memory-bound row kernels: LayerNorm, embedding gather (+ LayerNorm),
+// masked mean pool and L2 normalisation.
+//
+// For 384-wide rows one wavefront owns a row: lane l holds columns
+// 2l + 128j (j = 0, 1, 2) as three 4-byte half2 loads, so each load
+// instruction of the wavefront covers 256 contiguous bytes.  The row stays in
+// registers; mean and variance are two butterfly reductions over those
+// registers (two-pass, as src/kernels/layernorm.cu:32-49, but one global read
+// instead of three).
+
+#include "kernels.h"
+
+namespace bbh {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one row per wavefront, 256 threads
+
+__device__ __forceinline__ void ln_row384(float (&v)[6], float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 6; ++e) s += v[e];
+  const float mean = wave_sum(s) * (1.0f / kHidden);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 6; ++e) {
+    v[e] -= mean;
+    q += v[e] * v[e];
+  }
+  const float rstd = rsqrtf(wave_sum(q) * (1.0f / kHidden) + eps);
+#pragma unroll
+  for (int e = 0; e < 6; ++e) v[e] *= rstd;
+}
+
+__device__ __forceinline__ void store_affine384(f16* __restrict__ y, const float (&v)[6],
+                                                const f16* __restrict__ gamma,
+                                                const f16* __restrict__ beta, int lane) {
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int c = 2 * lane + 128 * j;
+    const f16x2 gv = *reinterpret_cast<const f16x2*>(gamma + c);
+    const f16x2 bv = *reinterpret_cast<const f16x2*>(beta + c);
+    f16x2 o;
+    o[0] = (f16)(v[2 * j] * (float)gv[0] + (float)bv[0]);
+    o[1] = (f16)(v[2 * j + 1] * (float)gv[1] + (float)bv[1]);
+    *reinterpret_cast<f16x2*>(y + c) = o;
+  }
+}
+
+// y = LN(x [+ residual]) for D == 384 (src/kernels/layernorm.cu:17-59).
+__global__ __launch_bounds__(256) void ln384_kernel(const f16* x, const f16* residual,
+                                                    const f16* __restrict__ gamma,
+                                                    const f16* __restrict__ beta, f16* y,
+                                                    int M, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const size_t off = (size_t)row * kHidden;
+  float v[6];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int c = 2 * lane + 128 * j;
+    const f16x2 a = *reinterpret_cast<const f16x2*>(x + off + c);
+    v[2 * j] = (float)a[0];
+    v[2 * j + 1] = (float)a[1];
+    if (residual) {
+      const f16x2 r = *reinterpret_cast<const f16x2*>(residual + off + c);
+      v[2 * j] += (float)r[0];
+      v[2 * j + 1] += (float)r[1];
+    }
+  }
+  ln_row384(v, eps);
+  store_affine384(y + off, v, gamma, beta, lane);
+}
+
+// Any D: three strided passes per wavefront-owned row, fp32 statistics.
+__global__ __launch_bounds__(256) void ln_generic_kernel(const f16* x, const f16* residual,
+                                                         const f16* __restrict__ gamma,
+                                                         const f16* __restrict__ beta, f16* y,
+                                                         int M, int D, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const size_t off = (size_t)row * D;
+  auto val = [&](int i) {
+    float v = (float)x[off + i];
+    if (residual) v += (float)residual[off + i];
+    return v;
+  };
+  float s = 0.f;
+  for (int i = lane; i < D; i += 64) s += val(i);
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float d = val(i) - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(wave_sum(q) / (float)D + eps);
+  for (int i = lane; i < D; i += 64)
+    y[off + i] = (f16)((val(i) - mean) * rstd * (float)gamma[i] + (float)beta[i]);
+}
+
+__device__ __forceinline__ int clamp_id(int v, int n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
+
+// out[row] = LN(word[id] + pos[row % seq] + type[tt]) (src/model/forward.cu:28-31;
+// gather as src/kernels/embedding.cu:20-30, sum kept in fp32 into the LN).
+__global__ __launch_bounds__(256) void embedding_ln_kernel(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ types,
+    const f16* __restrict__ word, const f16* __restrict__ pos, const f16* __restrict__ type,
+    const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* __restrict__ out, int M,
+    int seq, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const int id = clamp_id(ids[row], kVocab), tt = clamp_id(types[row], kTypes);
+  const f16* wr = word + (size_t)id * kHidden;
+  const f16* pr = pos + (size_t)(row % seq) * kHidden;
+  const f16* tr = type + (size_t)tt * kHidden;
+  float v[6];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int c = 2 * lane + 128 * j;
+    const f16x2 a = *reinterpret_cast<const f16x2*>(wr + c);
+    const f16x2 p = *reinterpret_cast<const f16x2*>(pr + c);
+    const f16x2 t = *reinterpret_cast<const f16x2*>(tr + c);
+    v[2 * j] = (float)a[0] + (float)p[0] + (float)t[0];
+    v[2 * j + 1] = (float)a[1] + (float)p[1] + (float)t[1];
+  }
+  ln_row384(v, eps);
+  store_affine384(out + (size_t)row * kHidden, v, gamma, beta, lane);
+}
+
+// Plain gather-sum, any hidden size (src/kernels/embedding.cu:8-31).
+__global__ __launch_bounds__(256) void embedding_kernel(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ types,
+    const f16* __restrict__ word, const f16* __restrict__ pos, const f16* __restrict__ type,
+    f16* __restrict__ out, int seq, int hidden, size_t total) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const size_t row = idx / hidden;
+  const int c = idx % hidden;
+  const int id = clamp_id(ids[row], kVocab), tt = clamp_id(types[row], kTypes);
+  const int p = row % seq;
+  out[idx] = (f16)((float)word[(size_t)id * hidden + c] + (float)pos[(size_t)p * hidden + c] +
+                   (float)type[(size_t)tt * hidden + c]);
+}
+
+// One workgroup per sentence: the four wavefronts sum disjoint sets of tokens
+// (rows w, w+4, ...) of the masked mean, combine through LDS, then wave 0
+// divides by max(count, 1) (src/kernels/pooling.cu:21-31) and scales by
+// 1 / max(||x||, 1e-12) (src/kernels/normalize.cu:7,29-30).
+__global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restrict__ hidden,
+                                                             const int32_t* __restrict__ mask,
+                                                             f16* __restrict__ out, int seq) {
+  __shared__ float part[4][kHidden];
+  __shared__ int cnt_part[4];
+  const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const f16* hb = hidden + (size_t)b * seq * kHidden;
+  const int32_t* mb = mask + (size_t)b * seq;
+  float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int cnt = 0;
+  for (int s = wave; s < seq; s += 4) {
+    if (mb[s] == 0) continue;
+    ++cnt;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const f16x2 a = *reinterpret_cast<const f16x2*>(hb + (size_t)s * kHidden + 2 * lane + 128 * j);
+      acc[2 * j] += (float)a[0];
+      acc[2 * j + 1] += (float)a[1];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    part[wave][2 * lane + 128 * j] = acc[2 * j];
+    part[wave][2 * lane + 128 * j + 1] = acc[2 * j + 1];
+  }
+  if (lane == 0) cnt_part[wave] = cnt;
+  __syncthreads();
+  if (wave != 0) return;
+  const int total = cnt_part[0] + cnt_part[1] + cnt_part[2] + cnt_part[3];
+  const float inv_cnt = 1.0f / (float)(total > 0 ? total : 1);
+  float v[6], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = 2 * lane + 128 * j + e;
+      v[2 * j + e] = (part[0][c] + part[1][c] + part[2][c] + part[3][c]) * inv_cnt;
+      ss += v[2 * j + e] * v[2 * j + e];
+    }
+  const float inv = 1.0f / fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    f16x2 o;
+    o[0] = (f16)(v[2 * j] * inv);
+    o[1] = (f16)(v[2 * j + 1] * inv);
+    *reinterpret_cast<f16x2*>(out + (size_t)b * kHidden + 2 * lane + 128 * j) = o;
+  }
+}
+
+// out[b, d] = masked mean over seq, any dim (src/kernels/pooling.cu:8-32).
+__global__ __launch_bounds__(256) void mean_pool_kernel(const f16* __restrict__ hidden,
+                                                        const int32_t* __restrict__ mask,
+                                                        f16* __restrict__ out, int batch,
+                                                        int seq, int dim) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= batch * dim) return;
+  const int b = idx / dim, d = idx % dim;
+  float acc = 0.f;
+  int cnt = 0;
+  for (int s = 0; s < seq; ++s) {
+    const int m = mask[(size_t)b * seq + s];
+    if (m) {
+      ++cnt;
+      acc += (float)hidden[((size_t)b * seq + s) * dim + d];
+    }
+  }
+  out[idx] = (f16)(acc / (float)(cnt > 0 ? cnt : 1));
+}
+
+// Rows of x /= max(||row||, 1e-12), one workgroup per row
+// (src/kernels/normalize.cu:10-33).
+__global__ __launch_bounds__(256) void l2_normalize_kernel(f16* x, int n) {
+  __shared__ float part[4];
+  f16* r = x + (size_t)blockIdx.x * n;
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float v = (float)r[i];
+    s += v * v;
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float inv = 1.0f / fmaxf(sqrtf(part[0] + part[1] + part[2] + part[3]), 1e-12f);
+  for (int i = threadIdx.x; i < n; i += 256) r[i] = (f16)((float)r[i] * inv);
+}
+
+}  // namespace
+
+hipError_t layernorm(const f16* x, const f16* residual, const f16* gamma, const f16* beta,
+                     f16* y, int M, int D, float eps, hipStream_t s) {
+  const dim3 grid((M + kRowsPerBlock - 1) / kRowsPerBlock);
+  const bool aligned = (((uintptr_t)x | (uintptr_t)residual | (uintptr_t)gamma |
+                         (uintptr_t)beta | (uintptr_t)y) & 3) == 0;
+  if (D == kHidden && aligned)
+    hipLaunchKernelGGL(ln384_kernel, grid, dim3(256), 0, s, x, residual, gamma, beta, y, M, eps);
+  else
+    hipLaunchKernelGGL(ln_generic_kernel, grid, dim3(256), 0, s, x, residual, gamma, beta, y, M,
+                       D, eps);
+  return hipGetLastError();
+}
+
+hipError_t embedding(const int32_t* ids, const int32_t* types, const f16* word, const f16* pos,
+                     const f16* type, f16* out, int batch, int seq, int hidden,
+                     hipStream_t s) {
+  const size_t total = (size_t)batch * seq * hidden;
+  hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     ids, types, word, pos, type, out, seq, hidden, total);
+  return hipGetLastError();
+}
+
+hipError_t embedding_ln(const int32_t* ids, const int32_t* types, const f16* word,
+                        const f16* pos, const f16* type, const f16* gamma, const f16* beta,
+                        f16* out, int batch, int seq, float eps, hipStream_t s) {
+  const int M = batch * seq;
+  hipLaunchKernelGGL(embedding_ln_kernel, dim3((M + kRowsPerBlock - 1) / kRowsPerBlock),
+                     dim3(256), 0, s, ids, types, word, pos, type, gamma, beta, out, M, seq,
+                     eps);
+  return hipGetLastError();
+}
+
+hipError_t mean_pool(const f16* hidden, const int32_t* mask, f16* out, int batch, int seq,
+                     int dim, hipStream_t s) {
+  hipLaunchKernelGGL(mean_pool_kernel, dim3((batch * dim + 255) / 256), dim3(256), 0, s, hidden,
+                     mask, out, batch, seq, dim);
+  return hipGetLastError();
+}
+
+hipError_t l2_normalize(f16* x, int n, int batch, hipStream_t s) {
+  hipLaunchKernelGGL(l2_normalize_kernel, dim3(batch), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
+hipError_t pool_normalize(const f16* hidden, const int32_t* mask, f16* out, int batch, int seq,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(pool_normalize_kernel, dim3(batch), dim3(256), 0, s, hidden, mask, out,
+                     seq);
+  return hipGetLastError();
+}
+
+}  // namespace bbh

@@ -1,0 +1,208 @@
+/*
+ * bbh.h - C ABI of the MI355X (gfx950) MiniLM-L6 sentence-embedding engine.
+ *
+ * This is the drop-in boundary for the reference's C++ host API
+ * (tytrdev/bert-by-hand, src/model/ and src/kernels/ headers).  The reference
+ * has no FFI layer of its own: its "operator API" is a set of C++ functions
+ * taking __half / int32 device pointers.  Each entry point below names the
+ * reference declaration it replaces.  A header-only C++ layer with the
+ * reference's own names (ModelWeights, Workspace, load_model_weights,
+ * make_workspace, bert_embed, ...) sits on top of this ABI in
+ * bert-by-hand_amd/cpp/bert_by_hand.hpp.
+ *
+ * Conventions
+ *  - All tensor arguments are DEVICE pointers.  fp16 data is IEEE binary16
+ *    (passed as void* / uint16_t*), indices and masks are int32, row-major,
+ *    and (batch, seq) inputs have row stride == seq.
+ *  - Every call only enqueues work on `stream` (a hipStream_t; NULL = the
+ *    null stream) and returns; the caller synchronises.  Nothing allocates
+ *    device memory after bbh_model_* / bbh_workspace_create.
+ *  - Every function returns a bbh_status.  On failure nothing is enqueued and
+ *    bbh_last_error() returns a message for the calling thread.  (The
+ *    reference instead prints and abort()s, src/core/cuda_check.h:7-17; the
+ *    C++ layer restores that behaviour.)
+ *  - A workspace must not be used by two calls that overlap in time.
+ */
+#ifndef BBH_H
+#define BBH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model constants: src/core/model_config.h:7-17. */
+#define BBH_VOCAB_SIZE 30522
+#define BBH_HIDDEN 384
+#define BBH_NUM_LAYERS 6
+#define BBH_NUM_HEADS 12
+#define BBH_HEAD_DIM 32
+#define BBH_FFN_DIM 1536
+#define BBH_MAX_POSITION 512
+#define BBH_TYPE_VOCAB_SIZE 2
+#define BBH_LAYER_NORM_EPS 1e-12f
+#define BBH_SEQ_ALIGN 16   /* seq must be a multiple of this (bench/bench.cu:63) */
+#define BBH_NUM_PARAMS 101 /* state_dict tensors without the pooler */
+
+typedef enum bbh_status {
+  BBH_OK = 0,
+  BBH_ERR_INVALID_ARG = 1, /* null pointer, non-positive size, bad index */
+  BBH_ERR_SEQ_ALIGN = 2,   /* seq % 16 != 0 */
+  BBH_ERR_CAPACITY = 3,    /* batch / seq above the workspace or model limit */
+  BBH_ERR_IO = 4,          /* weight file missing, unreadable or wrong size */
+  BBH_ERR_HIP = 5,         /* HIP runtime error (message has the HIP name) */
+  BBH_ERR_OOM = 6,         /* device allocation failed */
+  BBH_ERR_UNSUPPORTED = 7  /* shape the kernels do not handle */
+} bbh_status;
+
+typedef struct bbh_model bbh_model;         /* device-resident weights */
+typedef struct bbh_workspace bbh_workspace; /* device scratch for a forward */
+typedef void *bbh_stream_t;                 /* hipStream_t */
+
+/* ---- errors -------------------------------------------------------------- */
+const char *bbh_status_string(bbh_status s);
+/* Message of the last failed call on this thread ("" if none). */
+const char *bbh_last_error(void);
+const char *bbh_version(void);
+
+/* ---- parameter table ------------------------------------------------------ */
+/* The 101 tensors in HF state_dict order (scripts/dump_weights.py:75-83,
+ * src/model/weights.h:56-107).  Names are the reference file stems. */
+int bbh_param_count(void);
+const char *bbh_param_name(int index);
+size_t bbh_param_numel(int index);
+
+/* ---- weights --------------------------------------------------------------
+ * Replaces load_model_weights() (src/model/weights.h:88-107) with
+ * load_weight_fp16 / read_bin (src/core/loader.h:10-16,
+ * src/core/file_io.h:8-28): reads <dir>/<name>.bin raw little-endian fp16
+ * files, checks each file size exactly, fuses Q|K|V along the output
+ * dimension (src/model/weights.h:38-54) and uploads once.  Every file is read
+ * and checked before any device memory is touched. */
+bbh_status bbh_model_load_dir(const char *dir, bbh_model **out);
+/* Same, from host fp16 arrays: tensors[i] points at bbh_param_numel(i)
+ * binary16 values of tensor bbh_param_name(i). */
+bbh_status bbh_model_from_host(const uint16_t *const *tensors, int n_tensors,
+                               bbh_model **out);
+bbh_status bbh_model_free(bbh_model *m);
+size_t bbh_model_device_bytes(const bbh_model *m);
+
+/* ---- workspace ------------------------------------------------------------
+ * Replaces make_workspace(batch) (src/model/workspace.h:20-36).  The
+ * reference sizes every buffer for SEQ_LEN = 128 tokens per row; here
+ * max_seq is a runtime capacity (multiple of 16, at most 512) so batch 256 x
+ * seq 512 fits.  All scratch for any bbh_embed / bbh_encode with
+ * batch <= max_batch and seq <= max_seq is allocated here, once. */
+bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace **out);
+bbh_status bbh_workspace_free(bbh_workspace *ws);
+size_t bbh_workspace_bytes(int max_batch, int max_seq);
+/* Device pointer of the workspace's final-hidden buffer (batch*seq, 384)
+ * fp16: after bbh_embed it holds the encoder output, as ws.attn_out does
+ * after the reference's bert_embed (src/model/forward.cu:49). */
+void *bbh_workspace_hidden(bbh_workspace *ws);
+
+/* ---- the hot path ---------------------------------------------------------
+ * bert_embed (src/model/forward.h:17-19, src/model/forward.cu:44-53):
+ * embeddings -> 6 encoder layers -> masked mean pool -> L2 normalize.
+ * ids/types/mask: (batch, seq) int32.  emb: (batch, 384) fp16.
+ * seq is the runtime effective length, a multiple of 16, <= ws max_seq.
+ * Token ids must lie in [0, 30522) and types in {0, 1}; out-of-range values
+ * are clamped on the device rather than read out of bounds. */
+bbh_status bbh_embed(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
+                     const int32_t *types, const int32_t *mask, void *emb,
+                     int batch, int seq, bbh_stream_t stream);
+/* bert_encode (src/model/forward.h:11-13, forward.cu:20-42): final hidden
+ * states (batch*seq, 384) fp16 into out. */
+bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
+                      const int32_t *types, const int32_t *mask, void *out,
+                      int batch, int seq, bbh_stream_t stream);
+
+/* ---- block level (src/model/encoder.h:27-46) ------------------------------
+ * hidden / out: (batch*seq, 384) fp16, mask (batch, seq) int32; `layer`
+ * selects the model's encoder layer.  out may not alias hidden. */
+bbh_status bbh_attention_block(bbh_workspace *ws, const bbh_model *m, int layer,
+                               const void *hidden, const int32_t *mask, void *out,
+                               int batch, int seq, bbh_stream_t stream);
+bbh_status bbh_ffn_block(bbh_workspace *ws, const bbh_model *m, int layer,
+                         const void *hidden, void *out, int batch, int seq,
+                         bbh_stream_t stream);
+bbh_status bbh_encoder_layer(bbh_workspace *ws, const bbh_model *m, int layer,
+                             const void *hidden, const int32_t *mask, void *out,
+                             int batch, int seq, bbh_stream_t stream);
+
+/* ---- kernel level ---------------------------------------------------------- */
+/* launch_matmul (src/kernels/matmul.h:12-13): C(M,N) = A(M,K) . B(N,K)^T
+ * [+ bias(N)] [then exact-erf GELU]; fp16 in/out, fp32 accumulate.  Any
+ * M, N, K >= 1; the MFMA kernels take N % 64 == 0 and K % 64 == 0, other
+ * shapes go to a plain tiled kernel. */
+bbh_status bbh_linear(const void *A, const void *B, void *C, int M, int N, int K,
+                      const void *bias, int gelu, bbh_stream_t stream);
+/* Linear + bias + residual + LayerNorm in one kernel (the fused tail of
+ * attention_block / ffn_block, src/model/encoder.cu:47-50,61-64):
+ * y = LN(A . B^T + bias + residual) * gamma + beta, N must be 384.
+ * y may alias residual. */
+bbh_status bbh_linear_residual_layernorm(const void *A, const void *B,
+                                         const void *bias, const void *residual,
+                                         const void *gamma, const void *beta,
+                                         void *y, int M, int N, int K, float eps,
+                                         bbh_stream_t stream);
+/* launch_layernorm (src/kernels/layernorm.h:6-8): y = LN(x [+ residual]).
+ * Any D in [1, 4096]; y may alias x or residual. */
+bbh_status bbh_layernorm(const void *x, const void *gamma, const void *beta,
+                         void *y, int M, int D, float eps, const void *residual,
+                         bbh_stream_t stream);
+/* launch_embedding (src/kernels/embedding.h:9-12): out = word[id] +
+ * pos[row % seq] + type[tt], (batch*seq, hidden) fp16. */
+bbh_status bbh_embedding(const int32_t *ids, const int32_t *types,
+                         const void *word, const void *pos, const void *type,
+                         void *out, int seq, int hidden, int batch,
+                         bbh_stream_t stream);
+/* Embedding sum and the embedding LayerNorm fused (forward.cu:28-31),
+ * hidden must be 384. */
+bbh_status bbh_embedding_layernorm(const int32_t *ids, const int32_t *types,
+                                   const void *word, const void *pos,
+                                   const void *type, const void *gamma,
+                                   const void *beta, void *out, int seq,
+                                   int hidden, int batch, float eps,
+                                   bbh_stream_t stream);
+/* Masked multi-head attention straight out of the fused QKV activations:
+ * launch_attention_scores + launch_softmax(mask) + launch_attention_context
+ * (src/kernels/attention.h:9-18, softmax.h:11-12) as one kernel.
+ * qkv (batch*seq, 3*heads*head_dim) with Q|K|V column blocks, mask
+ * (batch, seq), merged (batch*seq, heads*head_dim).  head_dim must be 32,
+ * seq a multiple of 16 and <= 512. */
+bbh_status bbh_attention(const void *qkv, const int32_t *mask, void *merged,
+                         int batch, int heads, int seq, int head_dim, float scale,
+                         bbh_stream_t stream);
+/* launch_attention_scores (attention.h:9-11): scores(batch*heads, seq, seq)
+ * = scale * Q . K^T read strided from qkv (row stride qkv_stride, Q/K column
+ * offsets q_off/k_off).  seq % 16 == 0, head_dim == 32. */
+bbh_status bbh_attention_scores(const void *qkv, void *scores, int batch, int heads,
+                                int seq, int head_dim, int qkv_stride, int q_off,
+                                int k_off, float scale, bbh_stream_t stream);
+/* launch_softmax (softmax.h:11-12): row softmax in place over (M, N); with a
+ * mask, column j of row r is dropped when mask[(r / mask_stride) * N + j] ==
+ * 0 (mask_stride 0: one shared mask row). */
+bbh_status bbh_softmax(void *x, int M, int N, const int32_t *mask, int mask_stride,
+                       bbh_stream_t stream);
+/* launch_attention_context (attention.h:16-18): merged(batch*seq,
+ * heads*head_dim) = probs . V, V strided from qkv at column v_off. */
+bbh_status bbh_attention_context(const void *probs, const void *qkv, void *merged,
+                                 int batch, int heads, int seq, int head_dim,
+                                 int qkv_stride, int v_off, bbh_stream_t stream);
+/* launch_mean_pool (pooling.h:9-10): out(batch, dim) = masked mean. */
+bbh_status bbh_mean_pool(const void *hidden, const int32_t *mask, void *out,
+                         int seq, int dim, int batch, bbh_stream_t stream);
+/* launch_l2_normalize (normalize.h:7): rows of x /= max(||x||, 1e-12). */
+bbh_status bbh_l2_normalize(void *x, int n, int batch, bbh_stream_t stream);
+/* Masked mean pool + L2 normalize fused (forward.cu:51-52), dim 384. */
+bbh_status bbh_pool_normalize(const void *hidden, const int32_t *mask, void *out,
+                              int seq, int dim, int batch, bbh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BBH_H */

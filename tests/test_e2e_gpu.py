@@ -1,0 +1,200 @@
+"""End-to-end parity of bert_embed / bert_encode and the block-level entry
+points on the GPU against the fp32 oracle (the reference's fp32 torch forward,
+restated) and against transformers' BertModel golden vectors.
+
+Bar (north star): per-sentence embedding cosine >= 0.9999 against the fp32
+forward on the fp32 master weights; fp16 activations within 2e-2 max abs per
+kernel (block tests)."""
+
+import numpy as np
+import pytest
+
+from conftest import cosine_rows, to_dev
+from oracle import bert_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+COS = 0.9999
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _embed(torch, ws, model, ids, types, mask):
+    from bbh import engine
+
+    out = engine.bert_embed(ws, model, to_dev(torch, ids), to_dev(torch, types), to_dev(torch, mask))
+    return _np(out)
+
+
+@pytest.mark.parametrize("tag", ["s16", "rag"])
+def test_embed_matches_transformers_golden(torch_cuda, ws, model, golden_model, tag):
+    g = golden_model
+    got = _embed(torch_cuda, ws, model, g[f"{tag}_ids"], g[f"{tag}_types"], g[f"{tag}_mask"])
+    cos = cosine_rows(got, g[f"{tag}_embedding"])
+    assert cos.min() >= COS, cos
+    np.testing.assert_allclose(np.linalg.norm(got, axis=-1), 1.0, atol=2e-3)
+
+
+def test_encode_hidden_matches_transformers_golden(torch_cuda, ws, model, golden_model):
+    from bbh import engine
+
+    torch = torch_cuda
+    g = golden_model
+    ids, types, mask = g["rag_ids"], g["rag_types"], g["rag_mask"]
+    B, S = ids.shape
+    out = engine.bert_encode(ws, model, to_dev(torch, ids), to_dev(torch, types), to_dev(torch, mask))
+    got = _np(out).reshape(B, S, 384)
+    want = g["rag_hidden"]
+    real = mask.astype(bool)
+    cos = cosine_rows(got[real], want[real])
+    assert cos.min() >= COS
+    err = np.abs(got[real] - want[real])
+    assert err.mean() < 5e-3 and err.max() < 0.1
+
+
+def test_cfg2_batch64_seq16_rows(torch_cuda, ws, model, weights32):
+    from bbh import synth
+
+    ids, types, mask = synth.cfg_fixed(64, 16)
+    got = _embed(torch_cuda, ws, model, ids, types, mask)
+    want = O.bert_embed(weights32, ids[:1], types[:1], mask[:1])
+    assert cosine_rows(got, np.repeat(want, 64, 0)).min() >= COS
+    # identical rows -> identical embeddings, wherever they sit in the tiles
+    assert np.all(got == got[0])
+
+
+def test_cfg3_seq128_effective_length_invariance(torch_cuda, ws, model, weights32):
+    from bbh import synth
+
+    ids, types, mask = synth.cfg_fixed(64, 128)
+    e128 = _embed(torch_cuda, ws, model, ids, types, mask)
+    e16 = _embed(torch_cuda, ws, model, *synth.cfg_fixed(64, 16))
+    want = O.bert_embed(weights32, ids[:1], types[:1], mask[:1])
+    assert cosine_rows(e128, np.repeat(want, 64, 0)).min() >= COS
+    assert np.abs(e128 - e16).max() <= 2e-3  # README.md:80-83: padding does not change the embedding
+
+
+def test_cfg4_varlen_mix(torch_cuda, ws, model, weights32):
+    from bbh import synth
+
+    batches = synth.varlen_mix()
+    assert len(batches) == 32
+    checked = 0
+    for bi, (ids, types, mask, seq) in enumerate(batches):
+        got = _embed(torch_cuda, ws, model, ids, types, mask)
+        assert np.isfinite(got).all()
+        np.testing.assert_allclose(np.linalg.norm(got, axis=-1), 1.0, atol=2e-3)
+        if bi in (0, 5, 17, 31):  # oracle on a subset (largest eff 64 included)
+            want = O.bert_embed(weights32, ids, types, mask)
+            cos = cosine_rows(got, want)
+            assert cos.min() >= COS, (bi, cos.min())
+            checked += len(ids)
+    assert checked >= 64 * 3
+
+
+def test_cfg5_long_sequences(torch_cuda, ws, model, weights32):
+    from bbh import synth
+
+    ids, types, mask = synth.long_batch()
+    got = _embed(torch_cuda, ws, model, ids, types, mask)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(np.linalg.norm(got, axis=-1), 1.0, atol=2e-3)
+    # oracle on four sentences, each at its own effective length (invariance)
+    for b in (0, 77, 128, 255):
+        n = int(mask[b].sum())
+        s = synth.round16(n)
+        want = O.bert_embed(weights32, ids[b:b + 1, :s], types[b:b + 1, :s], mask[b:b + 1, :s])
+        assert cosine_rows(got[b:b + 1], want).min() >= COS
+
+
+def test_workspace_hidden_is_final_hidden(torch_cuda, ws, model, golden_model):
+    from bbh import engine
+
+    torch = torch_cuda
+    g = golden_model
+    ids, types, mask = (to_dev(torch, g[f"rag_{k}"]) for k in ("ids", "types", "mask"))
+    enc = engine.bert_encode(ws, model, ids, types, mask)
+    engine.bert_embed(ws, model, ids, types, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(ws.hidden(6, 32), enc)
+
+
+def test_blocks_layer0(torch_cuda, ws, model, weights32, golden_model):
+    from bbh import engine
+
+    torch = torch_cuda
+    g = golden_model
+    ids, types, mask = g["s16_ids"], g["s16_types"], g["s16_mask"]
+    emb = g["s16_emb_out"].reshape(16, 384)
+    hid = to_dev(torch, emb.astype(np.float16))
+    tm = to_dev(torch, mask)
+    out = torch.empty_like(hid)
+    engine.attention_block(ws, model, 0, hid, tm, out, 1, 16)
+    assert np.abs(_np(out) - g["s16_attn0_out"].reshape(16, 384)).max() <= 2e-2
+    out2 = torch.empty_like(hid)
+    engine.encoder_layer(ws, model, 0, hid, tm, out2, 1, 16)
+    assert np.abs(_np(out2) - g["s16_layer0_out"].reshape(16, 384)).max() <= 2e-2
+    # ffn_block alone on the attention output
+    out3 = torch.empty_like(hid)
+    engine.ffn_block(ws, model, 0, out, out3, 1, 16)
+    lw = O._layer(weights32, 0)
+    want = O.ffn_block(_np(out).reshape(1, 16, 384), lw).reshape(16, 384)
+    assert np.abs(_np(out3) - want).max() <= 2e-2
+
+
+def test_load_dir_equals_from_host(torch_cuda, ws, model, weights32, tmp_path, golden_model):
+    from bbh import engine, synth
+
+    synth.write_weights_dir(weights32, str(tmp_path))
+    m2 = engine.Model.load_dir(str(tmp_path))
+    g = golden_model
+    a = _embed(torch_cuda, ws, model, g["rag_ids"], g["rag_types"], g["rag_mask"])
+    b = _embed(torch_cuda, ws, m2, g["rag_ids"], g["rag_types"], g["rag_mask"])
+    m2.close()
+    assert np.array_equal(a, b)
+
+
+def test_out_of_range_ids_are_clamped(torch_cuda, ws, model, weights32):
+    from bbh import synth
+
+    ids, types, mask = synth.cfg_fixed(2, 16)
+    bad = ids.copy()
+    bad[0, 3] = 10 ** 6
+    bad[1, 3] = -5
+    t2 = types.copy()
+    t2[0, 1] = 7
+    got = _embed(torch_cuda, ws, model, bad, t2, mask)
+    fixed = ids.copy()
+    fixed[0, 3] = 30521
+    fixed[1, 3] = 0
+    tf = types.copy()
+    tf[0, 1] = 1
+    want = O.bert_embed(weights32, fixed, tf, mask)
+    assert cosine_rows(got, want).min() >= COS
+
+
+def test_error_statuses(torch_cuda, model):
+    from bbh import capi, engine, synth
+
+    torch = torch_cuda
+    small = engine.Workspace(4, 32)
+    ids, types, mask = (to_dev(torch, a) for a in synth.cfg_fixed(8, 32))
+    with pytest.raises(capi.BBHError) as e:
+        engine.bert_embed(small, model, ids, types, mask)
+    assert e.value.name == "BBH_ERR_CAPACITY"
+    ids2, types2, mask2 = (to_dev(torch, a) for a in synth.cfg_fixed(2, 48))
+    with pytest.raises(capi.BBHError) as e:
+        engine.bert_embed(small, model, ids2, types2, mask2)  # seq 48 > max_seq 32
+    assert e.value.name == "BBH_ERR_CAPACITY"
+    with pytest.raises(capi.BBHError) as e:
+        engine.bert_embed(small, model, ids2, types2, mask2, seq=24)
+    assert e.value.name == "BBH_ERR_SEQ_ALIGN"
+    # batch*seq within capacity at a shorter seq is accepted (row capacity)
+    ids3, types3, mask3 = (to_dev(torch, a) for a in synth.cfg_fixed(8, 16))
+    engine.bert_embed(small, model, ids3, types3, mask3)
+    torch.cuda.synchronize()
+    small.close()
+    L = capi.lib()
+    assert L.bbh_embed(None, model.handle, ids.data_ptr(), None, None, None, 1, 16, None) == 1

@@ -1,0 +1,273 @@
+"""Per-kernel parity of the HIP kernels against the CPU oracle, called through
+the C ABI.  Bar (north star): max abs error <= 2e-2 on fp16 activations; the
+reference's own cosine bars (tests/test_*.cu) are checked alongside."""
+
+import numpy as np
+import pytest
+
+from conftest import cosine_rows, to_dev
+from oracle import bert_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2  # max abs error on activations (north star)
+
+
+def _h(rng, shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float16)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+# ---- Linear ------------------------------------------------------------------
+
+GEMM_SHAPES = [
+    # (M, N, K, gelu): the four Linears of the path at small / ragged / large M
+    (16, 1152, 384, False), (48, 384, 384, False), (1040, 1536, 384, True),
+    (1024, 384, 1536, False), (3072, 1152, 384, False), (8192, 1536, 384, True),
+    (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
+]
+
+
+@pytest.mark.parametrize("M,N,K,gelu", GEMM_SHAPES)
+def test_linear(torch_cuda, M, N, K, gelu):
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(M * 7 + N + K)
+    A, W, b = _h(rng, (M, K)), _h(rng, (N, K), 1.0 / np.sqrt(K)), _h(rng, (N,), 0.1)
+    C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(to_dev(torch, A), to_dev(torch, W), C, M, N, K, bias=to_dev(torch, b),
+                         gelu=gelu)
+    want = O.linear(A.astype(np.float32), W.astype(np.float32), b.astype(np.float32), act_gelu=gelu)
+    got = _np(C)
+    assert np.abs(got - want).max() <= TOL
+    assert cosine_rows(got.ravel(), want.ravel()) >= 0.9999
+
+
+@pytest.mark.parametrize("tag", ["small", "real"])
+def test_linear_reference_kat(torch_cuda, kats, tag):
+    # tests/test_matmul.cu: 4x16x8 (any-shape kernel) and 128x384x384 (MFMA)
+    torch = torch_cuda
+    from bbh import engine
+
+    A, B, C = kats[f"matmul_{tag}_A"], kats[f"matmul_{tag}_B"], kats[f"matmul_{tag}_C"]
+    M, K = A.shape
+    N = B.shape[0]
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(to_dev(torch, A), to_dev(torch, B), out, M, N, K)
+    got = _np(out)
+    assert cosine_rows(got.ravel(), C.ravel()) >= 0.9995
+    assert np.abs(got - C).max() <= TOL
+
+
+@pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384)])
+def test_linear_residual_layernorm(torch_cuda, M, K):
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(M + K)
+    A, W = _h(rng, (M, K)), _h(rng, (384, K), 1.0 / np.sqrt(K))
+    b, r = _h(rng, (384,), 0.1), _h(rng, (M, 384))
+    g, be = (1 + rng.standard_normal(384) * 0.1).astype(np.float16), _h(rng, (384,), 0.1)
+    y = torch.empty((M, 384), dtype=torch.float16, device="cuda")
+    engine.launch_linear_residual_layernorm(to_dev(torch, A), to_dev(torch, W), to_dev(torch, b),
+                                            to_dev(torch, r), to_dev(torch, g), to_dev(torch, be),
+                                            y, M, K)
+    f = lambda a: a.astype(np.float32)  # noqa: E731
+    want = O.layer_norm(O.linear(f(A), f(W), f(b)), f(g), f(be), residual=f(r))
+    assert np.abs(_np(y) - want).max() <= TOL
+
+
+def test_linear_residual_layernorm_in_place(torch_cuda):
+    # y aliasing the residual is how the last layer writes the workspace's final hidden
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(3)
+    M, K = 200, 1536
+    A, W = _h(rng, (M, K)), _h(rng, (384, K), 1.0 / np.sqrt(K))
+    b, r = _h(rng, (384,), 0.1), _h(rng, (M, 384))
+    g, be = np.ones(384, np.float16), np.zeros(384, np.float16)
+    rt = to_dev(torch, r)
+    engine.launch_linear_residual_layernorm(to_dev(torch, A), to_dev(torch, W), to_dev(torch, b), rt,
+                                            to_dev(torch, g), to_dev(torch, be), rt, M, K)
+    f = lambda a: a.astype(np.float32)  # noqa: E731
+    want = O.layer_norm(O.linear(f(A), f(W), f(b)), f(g), f(be), residual=f(r))
+    assert np.abs(_np(rt) - want).max() <= TOL
+
+
+# ---- LayerNorm ---------------------------------------------------------------
+
+def test_layernorm_reference_kat(torch_cuda, kats):
+    torch = torch_cuda
+    from bbh import engine
+
+    x, g, b, y = kats["ln_x"], kats["ln_gamma"], kats["ln_beta"], kats["ln_y"]
+    out = torch.empty(x.shape, dtype=torch.float16, device="cuda")
+    engine.launch_layernorm(to_dev(torch, x), to_dev(torch, g), to_dev(torch, b), out, 128, 384)
+    got = _np(out)
+    assert cosine_rows(got.ravel(), y.ravel()) >= 0.9995
+    assert np.abs(got - y).max() <= TOL
+
+
+@pytest.mark.parametrize("D,res", [(384, True), (384, False), (100, True), (1536, False)])
+def test_layernorm(torch_cuda, D, res):
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(D)
+    M = 77
+    x, r = _h(rng, (M, D), 2.0), _h(rng, (M, D))
+    g, b = (1 + rng.standard_normal(D) * 0.1).astype(np.float16), _h(rng, (D,), 0.1)
+    out = torch.empty((M, D), dtype=torch.float16, device="cuda")
+    engine.launch_layernorm(to_dev(torch, x), to_dev(torch, g), to_dev(torch, b), out, M, D,
+                            residual=to_dev(torch, r) if res else None)
+    f = lambda a: a.astype(np.float32)  # noqa: E731
+    want = O.layer_norm(f(x), f(g), f(b), residual=f(r) if res else None)
+    assert np.abs(_np(out) - want).max() <= TOL
+
+
+# ---- embedding -----------------------------------------------------------------
+
+def test_embedding_and_fused_layernorm(torch_cuda, weights16):
+    torch = torch_cuda
+    from bbh import engine, synth
+
+    rows = [synth.sentence(np.random.default_rng(i), L) for i, L in enumerate([9, 30, 2, 48])]
+    ids, types, mask = synth.pack(rows, 48)
+    types[1, 5:] = 1
+    ids[3, 0] = 30521  # last vocabulary row
+    w = weights16
+    dw = {k: to_dev(torch, w[k].astype(np.float16)) for k in (
+        "embeddings.word_embeddings.weight", "embeddings.position_embeddings.weight",
+        "embeddings.token_type_embeddings.weight", "embeddings.LayerNorm.weight",
+        "embeddings.LayerNorm.bias")}
+    B, S = ids.shape
+    ti, tt = to_dev(torch, ids), to_dev(torch, types)
+    summed = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
+    engine.launch_embedding(ti, tt, dw["embeddings.word_embeddings.weight"],
+                            dw["embeddings.position_embeddings.weight"],
+                            dw["embeddings.token_type_embeddings.weight"], summed, S, 384, B)
+    want_sum = O.embedding_sum(ids, types, w["embeddings.word_embeddings.weight"],
+                               w["embeddings.position_embeddings.weight"],
+                               w["embeddings.token_type_embeddings.weight"]).reshape(B * S, 384)
+    assert np.abs(_np(summed) - want_sum).max() <= 1e-3
+    out = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
+    engine.launch_embedding_layernorm(ti, tt, dw["embeddings.word_embeddings.weight"],
+                                      dw["embeddings.position_embeddings.weight"],
+                                      dw["embeddings.token_type_embeddings.weight"],
+                                      dw["embeddings.LayerNorm.weight"], dw["embeddings.LayerNorm.bias"],
+                                      out, S, B)
+    want = O.embeddings(w, ids, types).reshape(B * S, 384)
+    assert np.abs(_np(out) - want).max() <= TOL
+
+
+# ---- attention -----------------------------------------------------------------
+
+def _masks(rng, B, S, kind):
+    m = np.zeros((B, S), np.int32)
+    if kind == "prefix":
+        for b in range(B):
+            m[b, :rng.integers(1, S + 1)] = 1
+    elif kind == "random":
+        m = (rng.random((B, S)) > 0.3).astype(np.int32)
+        m[:, 0] = 1
+    elif kind == "full":
+        m[:] = 1
+    elif kind == "empty_row":
+        for b in range(B):
+            m[b, :rng.integers(1, S + 1)] = 1
+        m[1] = 0  # every key of sequence 1 masked -> zero context (softmax.cu:57-62)
+    return m
+
+
+@pytest.mark.parametrize("S,kind", [(16, "prefix"), (32, "random"), (48, "empty_row"), (64, "full"),
+                                    (80, "prefix"), (128, "random"), (512, "prefix"),
+                                    (512, "empty_row")])
+def test_fused_attention(torch_cuda, S, kind):
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(S)
+    B = 3
+    qkv = _h(rng, (B, S, 1152), 1.5)
+    mask = _masks(rng, B, S, kind)
+    out = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
+    engine.launch_attention(to_dev(torch, qkv.reshape(B * S, 1152)), to_dev(torch, mask), out, B, S)
+    want = O.attention(qkv.astype(np.float32), mask).reshape(B * S, 384)
+    got = _np(out)
+    assert np.abs(got - want).max() <= TOL
+    if kind == "empty_row":
+        assert np.all(got[S:2 * S] == 0.0)
+
+
+def test_unfused_attention_pieces_match_fused(torch_cuda):
+    # launch_attention_scores -> launch_softmax(mask) -> launch_attention_context
+    # (src/model/encoder.cu:39-45) against the oracle and the fused kernel.
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(21)
+    B, S, H = 2, 48, 12
+    qkv = _h(rng, (B, S, 1152), 1.5)
+    mask = _masks(rng, B, S, "prefix")
+    tq, tm = to_dev(torch, qkv.reshape(B * S, 1152)), to_dev(torch, mask)
+    scale = 1.0 / np.sqrt(32)
+    scores = torch.empty((B * H, S, S), dtype=torch.float16, device="cuda")
+    engine.launch_attention_scores(tq, scores, B, H, S, 32, 1152, 0, 384, scale)
+    q = qkv[..., :384].astype(np.float32).reshape(B, S, H, 32).transpose(0, 2, 1, 3)
+    k = qkv[..., 384:768].astype(np.float32).reshape(B, S, H, 32).transpose(0, 2, 1, 3)
+    want_s = (q @ k.transpose(0, 1, 3, 2) * scale).reshape(B * H, S, S)
+    assert np.abs(_np(scores) - want_s).max() <= TOL
+    engine.launch_softmax(scores, B * H * S, S, tm, H * S)
+    want_p = O.masked_softmax(want_s.reshape(B, H, S, S), mask[:, None, None, :]).reshape(B * H, S, S)
+    assert np.abs(_np(scores) - want_p).max() <= 2e-3
+    merged = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
+    engine.launch_attention_context(scores, tq, merged, B, H, S, 32, 1152, 768)
+    want = O.attention(qkv.astype(np.float32), mask).reshape(B * S, 384)
+    assert np.abs(_np(merged) - want).max() <= TOL
+    fused = torch.empty_like(merged)
+    engine.launch_attention(tq, tm, fused, B, S)
+    assert np.abs(_np(fused) - _np(merged)).max() <= TOL
+
+
+def test_softmax_reference_kat(torch_cuda, kats):
+    torch = torch_cuda
+    from bbh import engine
+
+    x = to_dev(torch, kats["softmax_x"])
+    engine.launch_softmax(x, 128, 128)
+    got = _np(x)
+    assert cosine_rows(got.ravel(), kats["softmax_y"].ravel()) >= 0.9999
+    assert np.abs(got - kats["softmax_y"]).max() <= 2e-3
+
+
+# ---- pooling / normalize --------------------------------------------------------
+
+@pytest.mark.parametrize("B,S", [(1, 16), (5, 48), (64, 128), (3, 512)])
+def test_pool_normalize(torch_cuda, B, S):
+    torch = torch_cuda
+    from bbh import engine
+
+    rng = np.random.default_rng(B * S)
+    h = _h(rng, (B, S, 384))
+    mask = _masks(rng, B, S, "prefix")
+    if B > 2:
+        mask[2] = 0  # no real token -> zero embedding (pooling.cu:30, normalize.cu:30)
+    th, tm = to_dev(torch, h.reshape(B * S, 384)), to_dev(torch, mask)
+    f32 = h.astype(np.float32)
+    out = torch.empty((B, 384), dtype=torch.float16, device="cuda")
+    engine.launch_pool_normalize(th, tm, out, S, B)
+    want = O.l2_normalize(O.mean_pool(f32, mask))
+    got = _np(out)
+    assert np.abs(got - want).max() <= 2e-3
+    pooled = torch.empty((B, 384), dtype=torch.float16, device="cuda")
+    engine.launch_mean_pool(th, tm, pooled, S, 384, B)
+    assert np.abs(_np(pooled) - O.mean_pool(f32, mask)).max() <= 2e-3
+    engine.launch_l2_normalize(pooled, 384, B)
+    assert np.abs(_np(pooled) - want).max() <= 2e-3
+    if B > 2:
+        assert np.all(got[2] == 0.0)

@@ -494,7 +494,7 @@ bbh_status bbh_linear_residual_layernorm(const void* A, const void* B, const voi
     return fail(BBH_ERR_INVALID_ARG, "bbh_linear_residual_layernorm: null argument");
   if (M < 1 || K < 1) return fail(BBH_ERR_INVALID_ARG, "M and K must be positive");
   if (N != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "N must be 384");
-  if (K % 32 != 0) return fail(BBH_ERR_UNSUPPORTED, "K must be a multiple of 32");
+  if (K % 64 != 0) return fail(BBH_ERR_UNSUPPORTED, "K must be a multiple of 64");
   if (!aligned(A, 16) || !aligned(B, 16) || !aligned(bias, 8) || !aligned(residual, 8) ||
       !aligned(gamma, 8) || !aligned(beta, 8) || !aligned(y, 8))
     return misaligned("bbh_linear_residual_layernorm");

@@ -2,25 +2,34 @@
 //
 // Every Linear in the path is C(M,N) = A(M,K) . W(N,K)^T with the torch
 // (out, in) weight layout (reference: src/kernels/matmul.h:1-13), so both
-// operands are K-contiguous.  The kernels compute the transposed tile
-// D(n, m) = W . A^T with v_mfma_f32_16x16x32_f16: lane l then owns four
-// consecutive output columns n of one row m and stores them as one 8-byte
-// write.  fp16 operands, fp32 accumulation (the reference accumulates in
-// fp16 on GeForce, src/kernels/matmul.cu:97-110; CDNA4 runs fp32 accumulate at
-// full rate).
+// operands are K-contiguous.  fp16 operands, fp32 accumulation (the reference
+// accumulates in fp16 on GeForce, src/kernels/matmul.cu:97-110; CDNA4 runs
+// fp32 accumulate at full rate).
 //
-// Operand staging: a workgroup of 4 wavefronts owns a BM x BN output tile and
-// walks K in BK-wide slices.  Each slice of A and W is loaded from global
-// memory in 16-byte chunks into registers while the matrix cores work on the
-// previous slice, then written to the other half of a double-buffered LDS
-// area.  Inside LDS, chunk c of row r is stored at slot c ^ f(r) so the 16
-// rows read by one MFMA operand fetch fall into distinct bank groups.
+// Matrix-core instruction: v_mfma_f32_32x32x16_f16.  Measured on MI355X it
+// sustains ~2.15 PFLOP/s against ~1.44 for the 16x16x32 form, so every tile
+// here is built from 32x32 blocks.  The kernels compute the transposed tile
+// D(n, m) = W . A^T: lane l then holds, per 32x32 block, four runs of four
+// consecutive output columns n of one row m.
 //
-// Epilogues: bias (+ exact-erf GELU) as in src/kernels/matmul.cu:23-30, or
-// bias + residual + LayerNorm over the full 384-wide row, which folds the
-// reference's separate launch_layernorm(x, ..., residual) call
-// (src/model/encoder.cu:47-50, 61-64; src/kernels/layernorm.cu:17-59) into the
-// producing GEMM.
+// Operand pipeline: a workgroup of 4 wavefronts owns a BM x BN output tile
+// and walks K in 64-wide slices through a STAGES-deep ring of LDS buffers.
+// Slices are copied global -> LDS with global_load_lds_dwordx4 (16 bytes per
+// lane, no register staging), so STAGES-1 slices are in flight while the
+// matrix cores consume the current one; one barrier per slice.  Within a
+// slice, row r is 128 bytes = 8 chunks of 16 bytes and logical chunk c sits in
+// slot c ^ ((r >> 1) & 7): the 16 rows one MFMA operand fetch touches per
+// LDS cycle then hit 16 distinct bank groups.
+//
+// Tile order is XCD-aware: workgroup b runs on XCD b % 8, and the N-tiles of
+// one M-tile are given to consecutive workgroups of the same XCD so the A
+// rows are fetched from HBM once per XCD and re-read from that XCD's L2.
+//
+// Epilogues (fp32, then staged through LDS as fp16 for 16-byte coalesced
+// stores): bias; bias + exact-erf GELU (src/kernels/matmul.cu:23-30);
+// bias + residual; bias + residual + LayerNorm over the full 384-wide row
+// (folds the reference's separate launch_layernorm(x, ..., residual),
+// src/model/encoder.cu:47-50,61-64, src/kernels/layernorm.cu:17-59).
 
 #include "kernels.h"
 
@@ -29,231 +38,307 @@ namespace {
 
 constexpr int kThreads = 256;
 
-template <int BK>
-__device__ __forceinline__ int lds_off(int r, int c) {
-  if constexpr (BK == 64)
-    return r * 64 + ((c ^ (r & 7)) << 3);
-  else
-    return r * 32 + ((c ^ ((r >> 1) & 3)) << 3);
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
-struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-  static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile (rows m, cols n)
-  static constexpr int FM = TM / 16, FN = TN / 16;  // 16x16 MFMA tiles per wave
-  static constexpr int CPR = BK / 8;                // 16-byte chunks per row
-  static constexpr int A_CH = BM * CPR, W_CH = BN * CPR;
-  static constexpr int A_LD = (A_CH + kThreads - 1) / kThreads;
-  static constexpr int W_LD = (W_CH + kThreads - 1) / kThreads;
-  static constexpr int STAGE = (BM + BN) * BK;  // halves per pipeline stage
-  static constexpr size_t LDS = 2 * STAGE * sizeof(f16);
-  static_assert(WM * WN == 4, "four wavefronts per workgroup");
-  static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be 16-aligned");
-  static_assert(BK == 32 || BK == 64, "BK");
+// LDS layout of one K slice: BK halves per row, in 16-byte chunks; logical
+// chunk c of row r sits in slot c ^ f(r).  For BK = 64 (8 chunks) f(r) =
+// (r >> 1) & 7, for BK = 32 (4 chunks) f(r) = (r >> 2) & 3: either way the 16
+// rows an MFMA operand fetch reads per LDS cycle land in 16 distinct 16-byte
+// bank groups.  RPI = rows one 1 KB global_load_lds instruction fills.
+template <int BK>
+struct Slice;
+template <>
+struct Slice<64> {
+  static constexpr int CPR = 8, RPI = 8;
+  __device__ static __forceinline__ int f(int r) { return (r >> 1) & 7; }
+  __device__ static __forceinline__ int off(int r, int c) { return r * 64 + ((c ^ f(r)) << 3); }
+};
+template <>
+struct Slice<32> {
+  static constexpr int CPR = 4, RPI = 16;
+  __device__ static __forceinline__ int f(int r) { return (r >> 2) & 3; }
+  __device__ static __forceinline__ int off(int r, int c) { return r * 32 + ((c ^ f(r)) << 3); }
 };
 
-// K loop shared by all MFMA GEMMs.  On return acc[fm][fn] holds the fp32
-// product tile: lane (r16 = l%16, g = l/16) has D rows n = n0 + wn*TN + fn*16 +
-// 4g + i (i < 4) of column m = m0 + wm*TM + fm*16 + r16.  Rows of A past M are
-// read clamped to row M-1 (valid memory, results discarded by the caller).
-template <class T>
-__device__ __forceinline__ void mainloop(const f16* __restrict__ A,
-                                         const f16* __restrict__ W, int M, int K,
-                                         int m0, int n0, f16* smem,
-                                         f32x4 (&acc)[T::FM][T::FN]) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / T::WN, wn = wave % T::WN;
-  const int r16 = lane & 15, g = lane >> 4;
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
-  f16x8 ra[T::A_LD], rw[T::W_LD];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < T::A_LD; ++i) {
-      const int c = tid + i * kThreads;
-      if (T::A_CH % kThreads == 0 || c < T::A_CH) {
-        const int row = c / T::CPR, ch = c % T::CPR;
-        const int gm = min(m0 + row, M - 1);
-        ra[i] = *reinterpret_cast<const f16x8*>(A + (size_t)gm * K + k0 + ch * 8);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < T::W_LD; ++i) {
-      const int c = tid + i * kThreads;
-      if (T::W_CH % kThreads == 0 || c < T::W_CH) {
-        const int row = c / T::CPR, ch = c % T::CPR;
-        rw[i] = *reinterpret_cast<const f16x8*>(W + (size_t)(n0 + row) * K + k0 + ch * 8);
-      }
-    }
-  };
-  auto sstore = [&](int buf) {
-    f16* sA = smem + buf * T::STAGE;
-    f16* sW = sA + T::BM * T::BK;
-#pragma unroll
-    for (int i = 0; i < T::A_LD; ++i) {
-      const int c = tid + i * kThreads;
-      if (T::A_CH % kThreads == 0 || c < T::A_CH)
-        *reinterpret_cast<f16x8*>(sA + lds_off<T::BK>(c / T::CPR, c % T::CPR)) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < T::W_LD; ++i) {
-      const int c = tid + i * kThreads;
-      if (T::W_CH % kThreads == 0 || c < T::W_CH)
-        *reinterpret_cast<f16x8*>(sW + lds_off<T::BK>(c / T::CPR, c % T::CPR)) = rw[i];
-    }
-  };
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int BK_ = 64>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, BK = BK_;
+  using L = Slice<BK>;
+  static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
+  static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
+  static constexpr int ROWS = BM + BN;              // A rows then W rows in a stage
+  static constexpr int STAGE = ROWS * BK;           // halves per stage
+  static constexpr int LPT = ROWS / (4 * L::RPI);   // global_load_lds per thread per stage
+  static constexpr int OUT_LD = BN + 8;             // padded row of the fp16 output tile
+  static constexpr size_t RING = (size_t)STAGES * STAGE * sizeof(f16);
+  static constexpr size_t OUT = (size_t)BM * OUT_LD * sizeof(f16) + 8 * BM * sizeof(float);
+  static constexpr size_t LDS = RING > OUT ? RING : OUT;
+  static_assert(WM * WN == 4, "four wavefronts");
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is whole 32x32 blocks");
+  static_assert(ROWS % (4 * L::RPI) == 0 && BM % L::RPI == 0, "load distribution");
+  static_assert(STAGES >= 2, "pipeline depth");
+  static_assert(LPT * (STAGES - 2) < 64, "vmcnt range");
+};
 
-  const int KT = K / T::BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+// Issue the global -> LDS copies of one K slice.  Each wavefront instruction
+// fills 1 KB = RPI rows; lane i lands at row i / CPR, slot i % CPR of them.
+template <class C>
+__device__ __forceinline__ void issue_slice(const f16* __restrict__ A, const f16* __restrict__ W,
+                                            int M, int K, int m0, int n0, int k0, f16* buf) {
+  using L = typename C::L;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < C::LPT; ++j) {
+    const int g = wave * C::LPT + j;  // RPI-row group
+    const int r = g * L::RPI + lane / L::CPR;
+    const int sl = lane % L::CPR;
+    const int cl = sl ^ L::f(r);  // logical chunk that belongs in slot sl
+    const f16* src = (r < C::BM) ? A + (size_t)min(m0 + r, M - 1) * K + k0 + cl * 8
+                                 : W + (size_t)(n0 + r - C::BM) * K + k0 + cl * 8;
+    __builtin_amdgcn_global_load_lds(
+        src, (__attribute__((address_space(3))) void*)(buf + g * L::RPI * C::BK), 16, 0, 0);
+  }
+}
+
+template <class C>
+__device__ __forceinline__ void wait_slices(int pending) {
+  // pending = slices allowed to stay in flight (0 .. STAGES-2)
+  if constexpr (C::STAGES >= 4) {
+    if (pending >= 2) { wait_vm<C::LPT * 2>(); return; }
+  }
+  if constexpr (C::STAGES >= 3) {
+    if (pending >= 1) { wait_vm<C::LPT>(); return; }
+  }
+  wait_vm<0>();
+}
+
+// Scheduling groups: (one DS read, then ~Q/R MFMAs) x R.
+template <int R, int Q, int I = 0>
+__device__ __forceinline__ void interleave() {
+  if constexpr (I < R) {
+    constexpr int n = (I < Q % R) ? Q / R + 1 : Q / R;
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x008, n, 0);
+    interleave<R, Q, I + 1>();
+  }
+}
+
+// The K loop.  On return acc[fm][fn][i] = D(n, m) with
+//   n = n0 + wn*TN + fn*32 + 8*(i/4) + 4*(lane/32) + i%4,
+//   m = m0 + wm*TM + fm*32 + lane%32.
+template <class C>
+__device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* __restrict__ W,
+                                         int M, int K, int m0, int n0, f16* smem,
+                                         f32x16 (&acc)[C::FM][C::FN]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int r32 = lane & 31, kh = lane >> 5;
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[fm][fn][i] = 0.f;
+
+  const int KT = K / C::BK;
+#pragma unroll
+  for (int s = 0; s < C::STAGES - 1; ++s)
+    if (s < KT) issue_slice<C>(A, W, M, K, m0, n0, s * C::BK, smem + s * C::STAGE);
+
+  constexpr int KS = C::BK / 16;         // MFMA k-steps per slice
+  constexpr int R = C::FM + C::FN;       // LDS fragment reads per k-step
+  constexpr int Q = C::FM * C::FN;       // MFMAs per k-step
   for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * T::BK);
-    const f16* sA = smem + cur * T::STAGE;
-    const f16* sW = sA + T::BM * T::BK;
+    wait_slices<C>(min(C::STAGES - 2, KT - 1 - kt));
+    __syncthreads();  // slice kt visible to all; slice kt-1 fully consumed
+    const int nxt = kt + C::STAGES - 1;
+    if (nxt < KT)
+      issue_slice<C>(A, W, M, K, m0, n0, nxt * C::BK, smem + (nxt % C::STAGES) * C::STAGE);
+    const f16* sA = smem + (kt % C::STAGES) * C::STAGE;
+    const f16* sW = sA + C::BM * C::BK;
+    f16x8 a[2][C::FM], w[2][C::FN];
+    auto rd = [&](int s, f16x8(&aa)[C::FM], f16x8(&ww)[C::FN]) {
 #pragma unroll
-    for (int s = 0; s < T::BK / 32; ++s) {
-      f16x8 a[T::FM], w[T::FN];
+      for (int fm = 0; fm < C::FM; ++fm)
+        aa[fm] = *reinterpret_cast<const f16x8*>(sA + C::L::off(wm * C::TM + fm * 32 + r32, 2 * s + kh));
 #pragma unroll
-      for (int fm = 0; fm < T::FM; ++fm)
-        a[fm] = *reinterpret_cast<const f16x8*>(
-            sA + lds_off<T::BK>(wm * T::TM + fm * 16 + r16, s * 4 + g));
+      for (int fn = 0; fn < C::FN; ++fn)
+        ww[fn] = *reinterpret_cast<const f16x8*>(sW + C::L::off(wn * C::TN + fn * 32 + r32, 2 * s + kh));
+    };
+    rd(0, a[0], w[0]);
+    __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // all of step 0's reads first
 #pragma unroll
-      for (int fn = 0; fn < T::FN; ++fn)
-        w[fn] = *reinterpret_cast<const f16x8*>(
-            sW + lds_off<T::BK>(wn * T::TN + fn * 16 + r16, s * 4 + g));
+    for (int s = 0; s < KS; ++s) {
+      if (s + 1 < KS) rd(s + 1, a[(s + 1) & 1], w[(s + 1) & 1]);
 #pragma unroll
-      for (int fm = 0; fm < T::FM; ++fm)
+      for (int fm = 0; fm < C::FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < T::FN; ++fn) acc[fm][fn] = mfma16(w[fn], a[fm], acc[fm][fn]);
+        for (int fn = 0; fn < C::FN; ++fn)
+          acc[fm][fn] = mfma32(w[s & 1][fn], a[s & 1][fm], acc[fm][fn]);
+      if (s + 1 < KS)
+        interleave<R, Q>();  // spread the next step's R fragment reads over these Q MFMAs
+      else
+        __builtin_amdgcn_sched_group_barrier(0x008, Q, 0);
     }
-    if (kt + 1 < KT) sstore(cur ^ 1);
+  }
+  __syncthreads();  // ring free for the epilogue
+}
+
+// Tile coordinates from the workgroup id, XCD-aware (see header).
+__device__ __forceinline__ bool tile_of(int nb, int mb, int& mi, int& ni) {
+  const int b = blockIdx.x, x = b & 7, k = b >> 3;
+  ni = k % nb;
+  mi = (k / nb) * 8 + x;
+  return mi < mb;
+}
+
+// Write the fp16 tile staged in LDS (BM x OUT_LD) to C with 16-byte stores.
+template <class C>
+__device__ __forceinline__ void store_tile(const f16* tile, f16* __restrict__ out, int ldc, int M,
+                                           int m0, int n0) {
+  constexpr int CPR = C::BN / 8;
+  for (int idx = threadIdx.x; idx < C::BM * CPR; idx += kThreads) {
+    const int r = idx / CPR, c = idx % CPR;
+    if (m0 + r < M)
+      *reinterpret_cast<f16x8*>(out + (size_t)(m0 + r) * ldc + n0 + c * 8) =
+          *reinterpret_cast<const f16x8*>(tile + r * C::OUT_LD + c * 8);
+  }
+}
+
+template <class C, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(
+    const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
+    const f16* residual, const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* out,
+    int M, int N, int K, float eps) {
+  HIP_DYNAMIC_SHARED(f16, smem);
+  int mi, ni;
+  if (!tile_of(N / C::BN, (M + C::BM - 1) / C::BM, mi, ni)) return;
+  const int m0 = mi * C::BM, n0 = ni * C::BN;
+  f32x16 acc[C::FM][C::FN];
+  mainloop<C>(A, W, M, K, m0, n0, smem, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int r32 = lane & 31, kh = lane >> 5;
+  f16* tile = smem;  // BM x OUT_LD fp16
+  float* red = reinterpret_cast<float*>(smem + C::BM * C::OUT_LD);  // [2][4][BM]
+
+  if constexpr (EPI != kLayerNorm) {
+    // One 32x32 block at a time (bias, + GELU or + residual, to fp16 in LDS);
+    // the scheduling fence keeps a single block's values live.
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int ml = wm * C::TM + fm * 32 + r32;  // row inside the tile
+      const int mg = min(m0 + ml, M - 1);
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
+          const f16x4 bv = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
+          f16x4 rv = {0, 0, 0, 0};
+          if (EPI == kResidual) rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * N + n0 + nl);
+          f16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = acc[fm][fn][4 * j + i] + (float)bv[i] + (float)rv[i];
+            if (EPI == kGelu) v = gelu_as(v);
+            o[i] = (f16)v;
+          }
+          *reinterpret_cast<f16x4*>(tile + ml * C::OUT_LD + nl) = o;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    static_assert(C::BN == kHidden && C::WM == 1, "LayerNorm tile owns whole rows");
+    // v = acc + bias + residual
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int mg = min(m0 + fm * 32 + r32, M - 1);
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
+          const f16x4 bv = *reinterpret_cast<const f16x4*>(bias + n);
+          const f16x4 rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * kHidden + n);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[fm][fn][4 * j + i] += (float)bv[i] + (float)rv[i];
+        }
+    }
+    float mean[C::FM], rstd[C::FM];
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      float s = 0.f;
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s += acc[fm][fn][i];
+      s += __shfl_xor(s, 32, kWave);
+      if (kh == 0) red[wave * C::BM + fm * 32 + r32] = s;
+    }
     __syncthreads();
-  }
-}
-
-template <class T, bool kGelu>
-__global__ __launch_bounds__(kThreads) void gemm_bias_kernel(
-    const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
-    f16* __restrict__ C, int M, int N, int K) {
-  HIP_DYNAMIC_SHARED(f16, smem);
-  const int m0 = blockIdx.y * T::BM, n0 = blockIdx.x * T::BN;
-  f32x4 acc[T::FM][T::FN];
-  mainloop<T>(A, W, M, K, m0, n0, smem, acc);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / T::WN, wn = wave % T::WN;
-  const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    const int m = m0 + wm * T::TM + fm * 16 + r16;
-    if (m >= M) continue;
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int row = fm * 32 + r32;
+      mean[fm] = (red[row] + red[C::BM + row] + red[2 * C::BM + row] + red[3 * C::BM + row]) *
+                 (1.0f / kHidden);
+      float q = 0.f;
 #pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn) {
-      const int n = n0 + wn * T::TN + fn * 16 + g * 4;
-      f16x4 bv = bias ? *reinterpret_cast<const f16x4*>(bias + n) : f16x4{0, 0, 0, 0};
-      f16x4 o;
+      for (int fn = 0; fn < C::FN; ++fn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = acc[fm][fn][i] + (float)bv[i];
-        if (kGelu) v = gelu_erf(v);
-        o[i] = (f16)v;
+        for (int i = 0; i < 16; ++i) {
+          const float d = acc[fm][fn][i] - mean[fm];
+          q += d * d;
+        }
+      q += __shfl_xor(q, 32, kWave);
+      if (kh == 0) red[4 * C::BM + wave * C::BM + row] = q;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int row = fm * 32 + r32;
+      const float var = (red[4 * C::BM + row] + red[5 * C::BM + row] + red[6 * C::BM + row] +
+                         red[7 * C::BM + row]) *
+                        (1.0f / kHidden);
+      rstd[fm] = rsqrtf(var + eps);
+    }
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int ml = fm * 32 + r32;
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
+          const f16x4 gv = *reinterpret_cast<const f16x4*>(gamma + nl);
+          const f16x4 bv = *reinterpret_cast<const f16x4*>(beta + nl);
+          f16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] * (float)gv[i] + (float)bv[i]);
+          *reinterpret_cast<f16x4*>(tile + ml * C::OUT_LD + nl) = o;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      *reinterpret_cast<f16x4*>(C + (size_t)m * N + n) = o;
     }
-  }
-}
-
-// y = LN(A . W^T + bias + residual) over rows of exactly 384 columns.  The
-// workgroup owns BM full rows; the four wavefronts split the 384 columns
-// (96 each), and row statistics are combined through LDS.  Two-pass mean /
-// variance over the register-resident row, as src/kernels/layernorm.cu:32-49.
-template <class T>
-__global__ __launch_bounds__(kThreads) void gemm_ln_kernel(
-    const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
-    const f16* residual, const f16* __restrict__ gamma, const f16* __restrict__ beta,
-    f16* y, int M, int K, float eps) {
-  static_assert(T::BN == kHidden && T::WM == 1 && T::WN == 4, "row-owning tile");
-  HIP_DYNAMIC_SHARED(f16, smem);
-  const int m0 = blockIdx.x * T::BM;
-  f32x4 acc[T::FM][T::FN];
-  mainloop<T>(A, W, M, K, m0, 0, smem, acc);
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  float* red = reinterpret_cast<float*>(smem);  // [2][4][BM]; LDS is free after the K loop
-
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    const int mm = min(m0 + fm * 16 + r16, M - 1);
-#pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn) {
-      const int n = wave * T::TN + fn * 16 + g * 4;
-      const f16x4 bv = *reinterpret_cast<const f16x4*>(bias + n);
-      const f16x4 rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mm * kHidden + n);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[fm][fn][i] += (float)bv[i] + (float)rv[i];
-    }
-  }
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    float s = 0.f;
-#pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s += acc[fm][fn][i];
-    s = group4_sum(s);
-    if (g == 0) red[wave * T::BM + fm * 16 + r16] = s;
   }
   __syncthreads();
-  float mean[T::FM], rstd[T::FM];
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    const int row = fm * 16 + r16;
-    mean[fm] = (red[row] + red[T::BM + row] + red[2 * T::BM + row] + red[3 * T::BM + row]) *
-               (1.0f / kHidden);
-    float q = 0.f;
-#pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float d = acc[fm][fn][i] - mean[fm];
-        q += d * d;
-      }
-    q = group4_sum(q);
-    if (g == 0) red[4 * T::BM + wave * T::BM + row] = q;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    const int row = fm * 16 + r16;
-    const float var = (red[4 * T::BM + row] + red[5 * T::BM + row] + red[6 * T::BM + row] +
-                       red[7 * T::BM + row]) *
-                      (1.0f / kHidden);
-    rstd[fm] = rsqrtf(var + eps);
-  }
-#pragma unroll
-  for (int fm = 0; fm < T::FM; ++fm) {
-    const int m = m0 + fm * 16 + r16;
-    if (m >= M) continue;
-#pragma unroll
-    for (int fn = 0; fn < T::FN; ++fn) {
-      const int n = wave * T::TN + fn * 16 + g * 4;
-      const f16x4 gv = *reinterpret_cast<const f16x4*>(gamma + n);
-      const f16x4 bv = *reinterpret_cast<const f16x4*>(beta + n);
-      f16x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        o[i] = (f16)((acc[fm][fn][i] - mean[fm]) * rstd[fm] * (float)gv[i] + (float)bv[i]);
-      *reinterpret_cast<f16x4*>(y + (size_t)m * kHidden + n) = o;
-    }
-  }
+  store_tile<C>(tile, out, N, M, m0, n0);
 }
 
 // Any-shape fallback (the role of src/kernels/matmul.cu:34-59): 16x16 output
@@ -282,27 +367,91 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
   }
 }
 
-template <class K>
-hipError_t set_lds(K kernel, size_t bytes) {
-  if (bytes <= 65536) return hipSuccess;
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+template <class C, int EPI>
+hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residual,
+                  const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
+                  hipStream_t s) {
+  if constexpr (EPI == kLayerNorm && (C::BN != kHidden || C::WM != 1)) {
+    return hipErrorInvalidValue;  // LayerNorm needs a tile that owns whole rows
+  } else {
+    if (N % C::BN != 0) return hipErrorInvalidValue;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(gemm_kernel<C, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
+    if (attr != hipSuccess) return attr;
+    const int nb = N / C::BN, mb = (M + C::BM - 1) / C::BM;
+    const int grid = nb * 8 * ((mb + 7) / 8);
+    hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(kThreads), C::LDS, s, A, W, bias,
+                       residual, gamma, beta, out, M, N, K, eps);
+    return hipGetLastError();
+  }
 }
 
-template <class T, bool kGelu>
-hipError_t launch_bias(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N,
-                       int K, hipStream_t s) {
-  static hipError_t attr = set_lds(gemm_bias_kernel<T, kGelu>, T::LDS);
-  if (attr != hipSuccess) return attr;
-  dim3 grid(N / T::BN, (M + T::BM - 1) / T::BM);
-  hipLaunchKernelGGL((gemm_bias_kernel<T, kGelu>), grid, dim3(kThreads), T::LDS, s, A, W,
-                     bias, C, M, N, K);
-  return hipGetLastError();
+// Tile configurations (BM, BN, wavefronts M x N, pipeline stages, K slice),
+// by id.
+//   id  tile      wave tile  stages x BK   LDS
+//    0  64x64     32x32      4 x 64         64 KB
+//    1  64x128    32x64      4 x 64         96 KB
+//    2  128x64    64x32      4 x 64         96 KB
+//    3  128x128   64x64      3 x 64         96 KB
+//    4  256x128   128x64     2 x 64         96 KB
+//    5  128x384   128x96     2 x 64        128 KB   (owns whole 384-wide rows)
+//    6  64x384    64x96      2 x 64        112 KB   (owns whole rows)
+//    7  32x128    32x32      4 x 64         80 KB
+//    8  128x192   64x96      3 x 64        120 KB
+//    9  256x192   128x96     2 x 64        112 KB
+//   10  32x384    32x96      3 x 64        156 KB   (owns whole rows)
+//   11  128x384   128x96     4 x 32        128 KB   (owns whole rows)
+//   12  256x192   128x96     4 x 32        112 KB
+//   13  128x192   64x96      4 x 32         80 KB
+//   14  64x384    64x96      4 x 32        112 KB   (owns whole rows)
+//   15  256x128   128x64     4 x 32         96 KB
+//   16  128x128   64x64      6 x 32         96 KB
+template <int EPI>
+hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
+                     const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
+                     hipStream_t s) {
+#define BBH_CFG(ID, BM, BN, WM, WN, ST, BKV)                                                    \
+  case ID:                                                                                    \
+    return launch<Cfg<BM, BN, WM, WN, ST, BKV>, EPI>(A, W, bias, residual, gamma, beta, out, M, \
+                                                     N, K, eps, s);
+  switch (id) {
+    BBH_CFG(0, 64, 64, 2, 2, 4, 64)
+    BBH_CFG(1, 64, 128, 2, 2, 4, 64)
+    BBH_CFG(2, 128, 64, 2, 2, 4, 64)
+    BBH_CFG(3, 128, 128, 2, 2, 3, 64)
+    BBH_CFG(4, 256, 128, 2, 2, 2, 64)
+    BBH_CFG(5, 128, 384, 1, 4, 2, 64)
+    BBH_CFG(6, 64, 384, 1, 4, 2, 64)
+    BBH_CFG(7, 32, 128, 1, 4, 4, 64)
+    BBH_CFG(8, 128, 192, 2, 2, 3, 64)
+    BBH_CFG(9, 256, 192, 2, 2, 2, 64)
+    BBH_CFG(10, 32, 384, 1, 4, 3, 64)
+    BBH_CFG(11, 128, 384, 1, 4, 4, 32)
+    BBH_CFG(12, 256, 192, 2, 2, 4, 32)
+    BBH_CFG(13, 128, 192, 2, 2, 4, 32)
+    BBH_CFG(14, 64, 384, 1, 4, 4, 32)
+    BBH_CFG(15, 256, 128, 2, 2, 4, 32)
+    BBH_CFG(16, 128, 128, 2, 2, 6, 32)
+  }
+#undef BBH_CFG
+  return hipErrorInvalidValue;
 }
 
-using TileBig = Tile<128, 128, 64, 2, 2>;
-using TileSmall = Tile<64, 64, 64, 2, 2>;
-using TileLn = Tile<32, 384, 32, 1, 4>;
+// Tile choice per shape, from sweeps of every id at the path's shapes on
+// MI355X (M = 2048..8192 for the varlen batches, 131072 for batch 256 x 512).
+constexpr int kBnOf[] = {64, 128, 64, 128, 128, 384, 384, 128, 192, 192, 384, 384, 192, 192, 384, 128, 128};
+
+int pick_plain(int M, int N) {
+  int id;
+  if (M >= 16384)
+    id = (N == 1152) ? 9 : 13;
+  else if (M > 4096)
+    id = (N == 1152) ? 9 : (N == 384 ? 3 : 0);
+  else
+    id = (N == 1152) ? 3 : 0;
+  return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
+}
 
 }  // namespace
 
@@ -319,24 +468,48 @@ hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int 
                        gelu ? 1 : 0);
     return hipGetLastError();
   }
-  const bool big = (N % 128 == 0) && (size_t)M * N >= (size_t)256 * 128 * 128;
-  if (big)
-    return gelu ? launch_bias<TileBig, true>(A, W, bias, C, M, N, K, s)
-                : launch_bias<TileBig, false>(A, W, bias, C, M, N, K, s);
-  return gelu ? launch_bias<TileSmall, true>(A, W, bias, C, M, N, K, s)
-              : launch_bias<TileSmall, false>(A, W, bias, C, M, N, K, s);
+  const int id = pick_plain(M, N);
+  return gelu ? launch_id<kGelu>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s)
+              : launch_id<kBias>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s);
 }
 
-hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
-                            const f16* residual, const f16* gamma, const f16* beta,
-                            f16* y, int M, int K, float eps, hipStream_t s) {
-  using T = TileLn;
-  static hipError_t attr = set_lds(gemm_ln_kernel<T>, T::LDS);
-  if (attr != hipSuccess) return attr;
-  dim3 grid((M + T::BM - 1) / T::BM);
-  hipLaunchKernelGGL((gemm_ln_kernel<T>), grid, dim3(kThreads), T::LDS, s, A, W, bias,
-                     residual, gamma, beta, y, M, K, eps);
-  return hipGetLastError();
+hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f16* residual,
+                            const f16* gamma, const f16* beta, f16* y, int M, int K, float eps,
+                            hipStream_t s) {
+  // Large M: one kernel whose 128x384 tile owns whole rows.  Smaller M: a
+  // tile that owns whole rows leaves most CUs idle and streams all of W per
+  // workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
+  // (in place over y) and the row LayerNorm follows as its own pass.
+  if (M >= 16384)
+    return launch_id<kLayerNorm>(5, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
+  hipError_t e = launch_id<kResidual>(pick_plain(M, kHidden), A, W, bias, residual, nullptr,
+                                      nullptr, y, M, kHidden, K, eps, s);
+  if (e != hipSuccess) return e;
+  return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);
 }
+
+#ifdef BBH_TUNING
+// Tuning hook (built only with -DBBH_TUNING): run tile config `id` with
+// epilogue epi (0 bias, 1 gelu, 2 residual, 3 layernorm).
+extern "C" int bbh_tune_gemm(int id, int epi, const void* A, const void* W, const void* bias,
+                             const void* residual, const void* gamma, const void* beta, void* out,
+                             int M, int N, int K, float eps, void* stream) {
+  auto a = static_cast<const f16*>(A);
+  auto w = static_cast<const f16*>(W);
+  auto b = static_cast<const f16*>(bias);
+  auto r = static_cast<const f16*>(residual);
+  auto g = static_cast<const f16*>(gamma);
+  auto be = static_cast<const f16*>(beta);
+  auto o = static_cast<f16*>(out);
+  auto st = static_cast<hipStream_t>(stream);
+  switch (epi) {
+    case 0: return launch_id<kBias>(id, a, w, b, r, g, be, o, M, N, K, eps, st);
+    case 1: return launch_id<kGelu>(id, a, w, b, r, g, be, o, M, N, K, eps, st);
+    case 2: return launch_id<kResidual>(id, a, w, b, r, g, be, o, M, N, K, eps, st);
+    case 3: return launch_id<kLayerNorm>(id, a, w, b, r, g, be, o, M, N, K, eps, st);
+  }
+  return hipErrorInvalidValue;
+}
+#endif
 
 }  // namespace bbh

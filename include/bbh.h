@@ -141,8 +141,8 @@ bbh_status bbh_linear(const void *A, const void *B, void *C, int M, int N, int K
                       const void *bias, int gelu, bbh_stream_t stream);
 /* Linear + bias + residual + LayerNorm in one kernel (the fused tail of
  * attention_block / ffn_block, src/model/encoder.cu:47-50,61-64):
- * y = LN(A . B^T + bias + residual) * gamma + beta, N must be 384.
- * y may alias residual. */
+ * y = LN(A . B^T + bias + residual) * gamma + beta, N must be 384 and K a
+ * multiple of 64.  y may alias residual. */
 bbh_status bbh_linear_residual_layernorm(const void *A, const void *B,
                                          const void *bias, const void *residual,
                                          const void *gamma, const void *beta,

@@ -36,6 +36,10 @@ SIGNATURES = {
                           c_void_p]),
     "bbh_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                            c_void_p]),
+    "bbh_pool_create": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_void_p)]),
+    "bbh_pool_free": (c_int, [c_void_p]),
+    "bbh_embed_batches": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "bbh_attention_block": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int,
                                     c_int, c_void_p]),
     "bbh_ffn_block": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p]),

@@ -123,6 +123,57 @@ class _DeviceArray:
                                          "strides": None}
 
 
+class Pool:
+    """n HIP streams, each with its own workspace; embed_batches overlaps
+    independent batches across them (replaces a sequential batch loop)."""
+
+    def __init__(self, n_streams: int, max_batch: int, max_seq: int):
+        self.handle = ctypes.c_void_p()
+        call("bbh_pool_create", n_streams, max_batch, max_seq, ctypes.byref(self.handle))
+
+    def close(self):
+        if self.handle:
+            call("bbh_pool_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class PackedBatches:
+    """Batches packed back to back in device memory for embed_batches:
+    batch i = (ids, types, mask) of shape (B_i, S_i)."""
+
+    def __init__(self, batches):
+        torch = _torch()
+        sizes = [int(b[0].shape[0]) for b in batches]
+        seqs = [int(b[0].shape[1]) for b in batches]
+        toks = [b * s for b, s in zip(sizes, seqs)]
+        self.tok_offsets = np.concatenate([[0], np.cumsum(toks)[:-1]]).astype(np.int64)
+        self.emb_rows = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+        self.sizes = np.asarray(sizes, np.int32)
+        self.seqs = np.asarray(seqs, np.int32)
+        self.rows = int(sum(sizes))
+        cat = lambda k: torch.from_numpy(np.concatenate([np.asarray(b[k]).reshape(-1) for b in batches]).astype(np.int32)).cuda()  # noqa: E731
+        self.ids, self.types, self.mask = cat(0), cat(1), cat(2)
+        self.n = len(batches)
+
+
+def embed_batches(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=None):
+    """(rows, 384) fp16 embeddings of every packed batch, in batch order."""
+    torch = _torch()
+    if emb is None:
+        emb = torch.empty((packed.rows, HIDDEN), dtype=torch.float16, device="cuda")
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    call("bbh_embed_batches", pool.handle, w.handle, _ptr(packed.ids), _ptr(packed.types),
+         _ptr(packed.mask), p(packed.tok_offsets), p(packed.sizes), p(packed.seqs),
+         p(packed.emb_rows), _ptr(emb), packed.n, _stream(stream))
+    return emb
+
+
 def load_model_weights(weights_or_dir) -> Model:
     if isinstance(weights_or_dir, (str, bytes)):
         return Model.load_dir(weights_or_dir)

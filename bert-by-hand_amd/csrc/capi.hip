@@ -439,6 +439,106 @@ bbh_status bbh_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
   return run_encode(ws, m, ids, types, mask, static_cast<f16*>(out), batch, seq, S(stream));
 }
 
+struct bbh_pool {
+  std::vector<hipStream_t> streams;
+  std::vector<hipEvent_t> done;  // one per stream, recorded at the end of a call
+  hipEvent_t fork = nullptr;
+  std::vector<bbh_workspace*> ws;
+};
+
+static void pool_release(bbh_pool* p) {
+  for (auto w : p->ws) bbh_workspace_free(w);
+  for (auto e : p->done) (void)hipEventDestroy(e);
+  for (auto s : p->streams) (void)hipStreamDestroy(s);
+  if (p->fork) (void)hipEventDestroy(p->fork);
+  delete p;
+}
+
+bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool** out) {
+  if (!out) return fail(BBH_ERR_INVALID_ARG, "null out");
+  if (n_streams < 1 || n_streams > 64) return fail(BBH_ERR_INVALID_ARG, "n_streams must be in [1, 64]");
+  bbh_pool* p = new bbh_pool();
+  hipError_t e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    pool_release(p);
+    return hip_fail(e, "hipEventCreate");
+  }
+  for (int i = 0; i < n_streams; ++i) {
+    hipStream_t st;
+    e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);  // default priority
+    if (e != hipSuccess) {
+      pool_release(p);
+      return hip_fail(e, "hipStreamCreate");
+    }
+    p->streams.push_back(st);
+    hipEvent_t ev;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      pool_release(p);
+      return hip_fail(e, "hipEventCreate");
+    }
+    p->done.push_back(ev);
+    bbh_workspace* w = nullptr;
+    bbh_status st2 = bbh_workspace_create(max_batch, max_seq, &w);
+    if (st2 != BBH_OK) {
+      std::string msg = g_err;
+      pool_release(p);
+      return fail(st2, msg);
+    }
+    p->ws.push_back(w);
+  }
+  *out = p;
+  return BBH_OK;
+}
+
+bbh_status bbh_pool_free(bbh_pool* pool) {
+  if (!pool) return BBH_OK;
+  for (auto s : pool->streams) (void)hipStreamSynchronize(s);
+  pool_release(pool);
+  return BBH_OK;
+}
+
+bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* ids,
+                             const int32_t* types, const int32_t* mask,
+                             const int64_t* tok_offsets, const int* batch_sizes, const int* seqs,
+                             const int64_t* emb_rows, void* emb, int n_batches,
+                             bbh_stream_t stream) {
+  if (!pool || !m || !ids || !types || !mask || !tok_offsets || !batch_sizes || !seqs ||
+      !emb_rows || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed_batches: null argument");
+  if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
+  const int n = (int)pool->streams.size();
+  // validate everything before enqueueing anything
+  for (int i = 0; i < n_batches; ++i) {
+    bbh_status st = check_shape(pool->ws[i % n], batch_sizes[i], seqs[i]);
+    if (st != BBH_OK) return fail(st, "batch " + std::to_string(i) + ": " + g_err);
+    if (tok_offsets[i] < 0 || emb_rows[i] < 0)
+      return fail(BBH_ERR_INVALID_ARG, "batch " + std::to_string(i) + ": negative offset");
+  }
+  if (n_batches == 0) return BBH_OK;
+  const hipStream_t caller = S(stream);
+  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
+  const int used = n_batches < n ? n_batches : n;
+  for (int j = 0; j < used; ++j)
+    BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
+  for (int i = 0; i < n_batches; ++i) {
+    const int j = i % n;
+    const int64_t o = tok_offsets[i];
+    f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
+    bbh_workspace* w = pool->ws[j];
+    BBH_TRY(run_encode(w, m, ids + o, types + o, mask + o, w->attn_out, batch_sizes[i], seqs[i],
+                       pool->streams[j]));
+    BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out, mask + o, out, batch_sizes[i], seqs[i],
+                                             pool->streams[j]),
+                         "pool+normalize"));
+  }
+  for (int j = 0; j < used; ++j) {
+    BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
+    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
+  }
+  return BBH_OK;
+}
+
 static bbh_status check_layer(const bbh_workspace* ws, const bbh_model* m, int layer,
                               const void* hidden, const void* out, int batch, int seq) {
   if (!ws || !m || !hidden || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");

@@ -119,6 +119,27 @@ bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
                       const int32_t *types, const int32_t *mask, void *out,
                       int batch, int seq, bbh_stream_t stream);
 
+/* ---- many batches ---------------------------------------------------------
+ * A pool of n_streams HIP streams (default priority), each with its own
+ * workspace of (max_batch, max_seq).  bbh_embed_batches runs bert_embed on
+ * n_batches batches, dealing them round-robin to the pool streams so that
+ * independent batches overlap on the GPU; it replaces the reference's
+ * sequential corpus loop (bench/corpus.cu:64-77,120-132).  Batch i reads its
+ * (batch_sizes[i], seqs[i]) ids/types/mask starting at element
+ * tok_offsets[i] of the device arrays and writes batch_sizes[i] rows of emb
+ * starting at row emb_rows[i].  The size/offset arrays are HOST arrays.  The
+ * call orders itself after prior work on `stream` and makes later work on
+ * `stream` wait for all batches; it returns without a host sync.  A pool must
+ * not be used by two overlapping calls. */
+typedef struct bbh_pool bbh_pool;
+bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
+bbh_status bbh_pool_free(bbh_pool *pool);
+bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
+                             const int32_t *types, const int32_t *mask,
+                             const int64_t *tok_offsets, const int *batch_sizes,
+                             const int *seqs, const int64_t *emb_rows, void *emb,
+                             int n_batches, bbh_stream_t stream);
+
 /* ---- block level (src/model/encoder.h:27-46) ------------------------------
  * hidden / out: (batch*seq, 384) fp16, mask (batch, seq) int32; `layer`
  * selects the model's encoder layer.  out may not alias hidden. */

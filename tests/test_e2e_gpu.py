@@ -198,3 +198,24 @@ def test_error_statuses(torch_cuda, model):
     small.close()
     L = capi.lib()
     assert L.bbh_embed(None, model.handle, ids.data_ptr(), None, None, None, 1, 16, None) == 1
+
+
+def test_pool_embed_batches_equals_sequential(torch_cuda, ws, model):
+    # every batch of the varlen mix through a 3-stream pool == one bert_embed per batch
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    batches = synth.varlen_mix()[:11]
+    pool = engine.Pool(3, 64, 64)
+    packed = engine.PackedBatches([b[:3] for b in batches])
+    got = engine.embed_batches(pool, model, packed)
+    torch.cuda.synchronize()
+    want = np.concatenate([_embed(torch, ws, model, *b[:3]) for b in batches])
+    assert np.array_equal(_np(got), want)
+    # capacity errors are reported before anything is enqueued
+    small = engine.Pool(2, 64, 32)
+    first_big = next(i for i, b in enumerate(batches) if b[3] > 32)
+    with pytest.raises(Exception, match=f"CAPACITY: batch {first_big}: seq"):
+        engine.embed_batches(small, model, packed)
+    small.close()
+    pool.close()

@@ -1,152 +1,181 @@
 // Masked multi-head self-attention for head_dim 32, read straight out of the
-// fused QKV activations (row stride 3*384, Q | K | V column blocks,
+// fused QKV activations (row stride 3*heads*32, Q | K | V column blocks,
 // src/model/weights.h:38-54; strided reads as src/kernels/attention.cu:25-28,
-// 74-75) and written straight into the merged (B*S, 384) layout
+// 74-75) and written straight into the merged (B*S, heads*32) layout
 // (attention.cu:87-92).
 //
 // The reference materialises scores (B*12, S, S) in HBM, runs a separate
 // masked softmax over them and a third kernel for P.V
-// (src/model/encoder.cu:39-45).  Here one kernel does all three per
-// (batch, head, 16-query tile) with an online softmax, so scores never leave
-// the chip; at S = 512 the reference layout would be 1.6 GB per layer.
+// (src/model/encoder.cu:39-45).  Here one workgroup owns one (sequence, head):
+// it stages that head's K (row-major) and V (transposed, [dim][key]) in LDS
+// once, then each wavefront walks 32-query tiles with an online softmax, so
+// scores never leave the chip (at S = 512 the reference layout is 1.6 GB per
+// layer).
 //
-// Per wavefront: 16 queries.  Keys are staged through LDS in blocks of 64
-// (K row-major, V transposed to [dim][key]); each 32-key chunk costs
-//   2 x v_mfma_f32_16x16x32_f16 for S^T = K . Q^T  (all 32 head dims at once)
-//   online-softmax update in fp32 (exp2, scale folded with log2 e)
-//   2 x v_mfma_f32_16x16x32_f16 for O^T = V^T . P^T
-// The S^T accumulator of lane l holds query l%16 and keys 4(l/16)+i; the K
-// rows of the two S^T tiles are permuted so that lane l's eight scores are the
-// contiguous keys 8(l/16)..8(l/16)+7, which are exactly the eight k-values
-// lane l must feed as operand B of the P.V product.  P therefore goes from
-// accumulator to MFMA operand without leaving the lane.
+// Per 32-query x 32-key chunk a wavefront issues four
+// v_mfma_f32_32x32x16_f16: two for S^T = K . Q^T (head dims 0-15, 16-31) and
+// two for O^T = V^T . P^T (keys 0-15, 16-31).  The 32 K rows of a chunk are
+// loaded in the permuted order key_of_row(r) so that the sixteen S^T values a
+// lane receives (query lane%32; keys 16*(i/8) + 8*(lane/32) + i%8) are exactly
+// the two 8-key groups that lane must supply as operand B of the two P.V
+// MFMAs: probabilities go from accumulator to MFMA operand without leaving
+// the lane, and V^T is read with one 16-byte LDS load per MFMA.
 //
-// Mask semantics follow src/kernels/softmax.cu:35-62: keys with mask 0 are
-// dropped; a query whose keys are all masked gets a zero context.  Chunks of
-// 32 keys that are entirely masked are skipped (their contribution is exactly
-// zero).
+// Softmax in fp32, base 2: the 1/sqrt(32) scale (src/model/encoder.cu:28) and
+// log2(e) fold into one FMA before v_exp_f32; the row max needs one exchange
+// with lane ^ 32.  Mask semantics follow src/kernels/softmax.cu:35-62: keys
+// with mask 0 are dropped and a query whose keys are all masked gets a zero
+// context.  32-key chunks are classified once per workgroup: fully masked
+// chunks are skipped (their contribution is exactly zero), fully unmasked
+// chunks need no mask arithmetic.
 
 #include "kernels.h"
 
 namespace bbh {
 namespace {
 
-constexpr int KB = 64;        // keys staged per LDS block
-constexpr int VT_LD = KB + 8;  // padded row of the transposed V tile
+// Key (within a 32-key chunk) loaded as row r of the S^T tile.
+__device__ __forceinline__ int key_of_row(int r) {
+  const int a = r >> 3, c = (r >> 2) & 1, b = r & 3;
+  return 16 * (a >> 1) + 8 * c + 4 * (a & 1) + b;
+}
 
-// Slot of 16-byte chunk c (of 4) in K-tile row j; conflict-free for the key
-// pattern one S^T operand fetch touches (rows {0,1,2,3,8,9,10,11} + const).
-__device__ __forceinline__ int k_off(int j, int c) {
-  const int sw = ((j >> 1) & 1) | ((j >> 2) & 2);
-  return j * 32 + ((c ^ sw) << 3);
+// Halves offset of 16-byte chunk c (8 head dims) of key row `key` in the K
+// tile; the XOR keeps the 16 rows of one operand fetch on distinct banks.
+__device__ __forceinline__ int ks_off(int key, int c) {
+  return key * 32 + ((c ^ ((key >> 2) & 3)) << 3);
+}
+
+size_t attn_lds_bytes(int seq) {
+  const int seqp = (seq + 31) & ~31;
+  return (size_t)seqp * 32 * 2 + (size_t)32 * (seqp + 8) * 2 + (size_t)seqp * 4 +
+         (size_t)(seqp / 32) * 4;
 }
 
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void attention_kernel(const f16* __restrict__ qkv,
                                                             const int32_t* __restrict__ mask,
-                                                            f16* __restrict__ out, int seq,
-                                                            int heads, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) f16 Ks[KB * 32];
-  __shared__ __attribute__((aligned(16))) f16 Vt[32 * VT_LD];
-  __shared__ float mb[KB];
-
-  const int b = blockIdx.z, h = blockIdx.y;
+                                                            f16* __restrict__ out, int batch,
+                                                            int seq, int heads, float c) {
+  HIP_DYNAMIC_SHARED(f16, smem);
+  // (sequence, head) of this workgroup; all heads of a sequence go to one XCD
+  // (workgroup id % 8) back to back, so its QKV rows are fetched into one L2.
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int b = (k / heads) * 8 + x, h = k % heads;
+  if (b >= batch) return;
+  const int seqp = (seq + 31) & ~31, nch = seqp >> 5, VLD = seqp + 8;
+  f16* Ks = smem;                                          // [seqp][32]
+  f16* Vt = Ks + seqp * 32;                                // [32][VLD]
+  float* mb = reinterpret_cast<float*>(Vt + 32 * VLD);     // [seqp]: 0 or -inf
+  int* cf = reinterpret_cast<int*>(mb + seqp);             // [nch]: 0 masked, 1 open, 2 mixed
   const int hid = heads * kHeadDim, ld = 3 * hid;
-  const f16* base = qkv + (size_t)b * seq * ld;
-  const int32_t* mrow_ptr = mask + (size_t)b * seq;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, g = lane >> 4;
-  const int q0 = (blockIdx.x * NW + wave) * 16;
-  const bool active = q0 < seq;
-  const int q = min(q0 + r16, seq - 1);
+  const f16* base = qkv + (size_t)b * seq * ld + h * kHeadDim;
+  const int tid = threadIdx.x;
+  constexpr int NT = 64 * NW;
 
-  const f16x8 qf = *reinterpret_cast<const f16x8*>(base + (size_t)q * ld + h * kHeadDim + g * 8);
-  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-  float mrun = -INFINITY, lsum = 0.f;
-
-  for (int kb = 0; kb < seq; kb += KB) {
-    __syncthreads();  // previous block's LDS reads are done
-    for (int c = tid; c < KB * 4; c += 64 * NW) {
-      const int j = c >> 2, ch = c & 3, key = kb + j;
-      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-      if (key < seq) {
-        const f16* row = base + (size_t)key * ld + h * kHeadDim + ch * 8;
-        kv = *reinterpret_cast<const f16x8*>(row + hid);
-        vv = *reinterpret_cast<const f16x8*>(row + 2 * hid);
-      }
-      *reinterpret_cast<f16x8*>(&Ks[k_off(j, ch)]) = kv;
+  for (int i = tid; i < seqp * 4; i += NT) {  // K: 16 bytes per (key, 8 dims)
+    const int key = i >> 2, ch = i & 3;
+    f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (key < seq) v = *reinterpret_cast<const f16x8*>(base + (size_t)key * ld + hid + ch * 8);
+    *reinterpret_cast<f16x8*>(Ks + ks_off(key, ch)) = v;
+  }
+  for (int i = tid; i < (seqp / 4) * 8; i += NT) {  // V^T: a 4-key x 4-dim block per thread
+    const int dq = i & 7, kq = i >> 3;
+    f16x4 r[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_LD + j] = vv[e];
+    for (int e = 0; e < 4; ++e) {
+      const int key = 4 * kq + e;
+      r[e] = key < seq ? *reinterpret_cast<const f16x4*>(base + (size_t)key * ld + 2 * hid + 4 * dq)
+                       : f16x4{0, 0, 0, 0};
     }
-    for (int j = tid; j < KB; j += 64 * NW) {
-      const int key = kb + j;
-      mb[j] = (key < seq && mrow_ptr[key] != 0) ? 0.f : -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f16x4 col = {r[0][e], r[1][e], r[2][e], r[3][e]};
+      *reinterpret_cast<f16x4*>(Vt + (4 * dq + e) * VLD + 4 * kq) = col;
     }
-    __syncthreads();
-    if (!active) continue;
+  }
+  for (int j = tid; j < seqp; j += NT)
+    mb[j] = (j < seq && mask[(size_t)b * seq + j] != 0) ? 0.f : -INFINITY;
+  __syncthreads();
+  for (int ch = tid; ch < nch; ch += NT) {
+    int on = 0;
+    for (int j = 0; j < 32; ++j) on += (mb[ch * 32 + j] == 0.f);
+    cf[ch] = on == 0 ? 0 : (on == 32 ? 1 : 2);
+  }
+  __syncthreads();
 
-    const int kend = min(KB, seq - kb);
-    for (int kc = 0; kc < kend; kc += 32) {
-      float mk[8];
-      bool any = false;
+  const int wave = tid >> 6, lane = tid & 63, r32 = lane & 31, kh = lane >> 5;
+  const int krow = key_of_row(r32);
+  const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int qt = wave; qt < nch; qt += NW) {
+    const int q = qt * 32 + r32;
+    const f16* qrow = base + (size_t)min(q, seq - 1) * ld;
+    const f16x8 q0 = *reinterpret_cast<const f16x8*>(qrow + 8 * kh);
+    const f16x8 q1 = *reinterpret_cast<const f16x8*>(qrow + 16 + 8 * kh);
+    f32x16 o = zero;
+    float m = -INFINITY, l = 0.f;
+    for (int kc = 0; kc < nch; ++kc) {
+      const int flag = cf[kc];
+      if (flag == 0) continue;
+      const int key = kc * 32 + krow;
+      const f16x8 k0 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, kh));
+      const f16x8 k1 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, 2 + kh));
+      f32x16 s = mfma32(k0, q0, zero);
+      s = mfma32(k1, q1, s);  // s[i]: key kc*32 + 16*(i/8) + 8*kh + i%8, query q (raw)
+      if (flag == 2) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        mk[e] = mb[kc + 8 * g + e];
-        any |= (mk[e] == 0.f);
+        for (int i = 0; i < 16; ++i) s[i] += mb[kc * 32 + 16 * (i >> 3) + 8 * kh + (i & 7)];
       }
-      if (!__any(any)) continue;
-
-      // S^T tiles: operand-A row r16 of tile t is key kc + 8(r16/4) + 4t + r16%4.
-      const int kr0 = kc + 8 * (r16 >> 2) + (r16 & 3);
-      const f16x8 k0 = *reinterpret_cast<const f16x8*>(&Ks[k_off(kr0, g)]);
-      const f16x8 k1 = *reinterpret_cast<const f16x8*>(&Ks[k_off(kr0 + 4, g)]);
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 s0 = mfma16(k0, qf, zero);  // keys kc+8g+i
-      const f32x4 s1 = mfma16(k1, qf, zero);  // keys kc+8g+4+i
-
-      float sv[8];
+      float mx = s[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sv[i] = s0[i] * scale_log2 + mk[i];
-        sv[4 + i] = s1[i] * scale_log2 + mk[4 + i];
-      }
-      float cmax = sv[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) cmax = fmaxf(cmax, sv[e]);
-      cmax = group4_max(cmax);
-      const float mnew = fmaxf(mrun, cmax);
-      const float muse = (mnew == -INFINITY) ? 0.f : mnew;
-      const float corr = exp2f(mrun - muse);
-      f16x8 p;
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mn = fmaxf(m, mx);  // finite: the chunk has an unmasked key
+      const float mc = mn * c;
+      const float corr = __builtin_amdgcn_exp2f(m * c - mc);
+      f16x8 pa, pb;
       float ps = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = exp2f(sv[e] - muse);
-        ps += pe;
-        p[e] = (f16)pe;
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i], c, -mc));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[8 + i], c, -mc));
+        ps += p0 + p1;
+        pa[i] = (f16)p0;
+        pb[i] = (f16)p1;
       }
-      lsum = lsum * corr + ps;
-      mrun = mnew;
-      o0 *= corr;
-      o1 *= corr;
-      const f16x8 v0 = *reinterpret_cast<const f16x8*>(&Vt[r16 * VT_LD + kc + 8 * g]);
-      const f16x8 v1 = *reinterpret_cast<const f16x8*>(&Vt[(16 + r16) * VT_LD + kc + 8 * g]);
-      o0 = mfma16(v0, p, o0);  // dims 4g+i of query r16
-      o1 = mfma16(v1, p, o1);  // dims 16+4g+i
+      l = l * corr + ps;
+      o *= corr;
+      const f16* vrow = Vt + r32 * VLD + kc * 32 + 8 * kh;
+      o = mfma32(*reinterpret_cast<const f16x8*>(vrow), pa, o);
+      o = mfma32(*reinterpret_cast<const f16x8*>(vrow + 16), pb, o);
+      m = mn;
+    }
+    const float lt = l + __shfl_xor(l, 32, kWave);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
+      f16* dst = out + ((size_t)b * seq + q) * hid + h * kHeadDim + 4 * kh;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
+        *reinterpret_cast<f16x4*>(dst + 8 * j) = w;
+      }
     }
   }
-  if (!active) return;
-  const float lt = group4_sum(lsum);
-  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  f16x4 w0, w1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w0[i] = (f16)(o0[i] * inv);
-    w1[i] = (f16)(o1[i] * inv);
-  }
-  f16* dst = out + ((size_t)b * seq + q0 + r16) * hid + h * kHeadDim + 4 * g;
-  *reinterpret_cast<f16x4*>(dst) = w0;
-  *reinterpret_cast<f16x4*>(dst + 16) = w1;
+}
+
+template <int NW>
+hipError_t launch_attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
+                            int heads, int seq, float c, hipStream_t s) {
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(attention_kernel<NW>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)attn_lds_bytes(kMaxPos));
+  if (attr != hipSuccess) return attr;
+  const int grid = heads * 8 * ((batch + 7) / 8);
+  hipLaunchKernelGGL((attention_kernel<NW>), dim3(grid), dim3(64 * NW), attn_lds_bytes(seq), s,
+                     qkv, mask, merged, batch, seq, heads, c);
+  return hipGetLastError();
 }
 
 // ---- unfused pieces with the reference's launcher shapes -------------------
@@ -216,17 +245,12 @@ __global__ __launch_bounds__(256) void context_kernel(const f16* __restrict__ pr
 
 hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
                      int seq, float scale, hipStream_t s) {
-  const float scale_log2 = scale * 1.4426950408889634f;
-  if (seq >= 64) {
-    dim3 grid((seq + 63) / 64, heads, batch);
-    hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, s, qkv, mask, merged, seq,
-                       heads, scale_log2);
-  } else {
-    dim3 grid(seq / 16, heads, batch);
-    hipLaunchKernelGGL(attention_kernel<1>, grid, dim3(64), 0, s, qkv, mask, merged, seq,
-                       heads, scale_log2);
-  }
-  return hipGetLastError();
+  const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
+  const int tiles = (seq + 31) / 32;            // 32-query tiles per sequence
+  if (tiles >= 8) return launch_attention<8>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles >= 4) return launch_attention<4>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles >= 2) return launch_attention<2>(qkv, mask, merged, batch, heads, seq, c, s);
+  return launch_attention<1>(qkv, mask, merged, batch, heads, seq, c, s);
 }
 
 hipError_t attention_scores(const f16* qkv, f16* scores, int batch, int heads, int seq,

@@ -13,13 +13,14 @@
 // consecutive output columns n of one row m.
 //
 // Operand pipeline: a workgroup of 4 wavefronts owns a BM x BN output tile
-// and walks K in 64-wide slices through a STAGES-deep ring of LDS buffers.
-// Slices are copied global -> LDS with global_load_lds_dwordx4 (16 bytes per
-// lane, no register staging), so STAGES-1 slices are in flight while the
-// matrix cores consume the current one; one barrier per slice.  Within a
-// slice, row r is 128 bytes = 8 chunks of 16 bytes and logical chunk c sits in
-// slot c ^ ((r >> 1) & 7): the 16 rows one MFMA operand fetch touches per
-// LDS cycle then hit 16 distinct bank groups.
+// and walks K in 64-wide slices.  Slices are copied global -> LDS with
+// global_load_lds_dwordx4 (16 bytes per lane, no register staging) into two
+// rings: the activations A, streamed from HBM, run SA-1 slices ahead (their
+// HBM latency is what a single shared ring exposes), the weights W, resident
+// in L2, one slice ahead; one barrier per slice.  Within a slice, row r is
+// 128 bytes = 8 chunks of 16 bytes and logical chunk c sits in slot
+// c ^ ((r >> 1) & 7): the 16 rows one MFMA operand fetch touches per LDS cycle
+// then hit 16 distinct bank groups.
 //
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and the N-tiles of
 // one M-tile are given to consecutive workgroups of the same XCD so the A
@@ -36,32 +37,17 @@
 namespace bbh {
 namespace {
 
-constexpr int kThreads = 256;
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// LDS layout of one K slice: BK halves per row, in 16-byte chunks; logical
-// chunk c of row r sits in slot c ^ f(r).  For BK = 64 (8 chunks) f(r) =
-// (r >> 1) & 7, for BK = 32 (4 chunks) f(r) = (r >> 2) & 3: either way the 16
-// rows an MFMA operand fetch reads per LDS cycle land in 16 distinct 16-byte
-// bank groups.  RPI = rows one 1 KB global_load_lds instruction fills.
+// LDS layout of one 64-wide K slice: 128 bytes = 8 chunks of 16 bytes per
+// row; logical chunk c of row r sits in slot c ^ f(r), f(r) = (r >> 1) & 7, so
+// the 16 rows an MFMA operand fetch reads per LDS cycle land in 16 distinct
+// 16-byte bank groups.
 template <int BK>
 struct Slice;
 template <>
 struct Slice<64> {
-  static constexpr int CPR = 8, RPI = 8;
   __device__ static __forceinline__ int f(int r) { return (r >> 1) & 7; }
   __device__ static __forceinline__ int off(int r, int c) { return r * 64 + ((c ^ f(r)) << 3); }
-};
-template <>
-struct Slice<32> {
-  static constexpr int CPR = 4, RPI = 16;
-  __device__ static __forceinline__ int f(int r) { return (r >> 2) & 3; }
-  __device__ static __forceinline__ int off(int r, int c) { return r * 32 + ((c ^ f(r)) << 3); }
 };
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
@@ -73,56 +59,54 @@ __device__ __forceinline__ void wait_vm() {
 
 enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int BK_ = 64>
+constexpr size_t kLdsMax = 160 * 1024;
+
+template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, BK = BK_;
-  using L = Slice<BK>;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SA = SA_, SW = 2, BK = 64;
+  static constexpr int PD = PD_;  // > 0: register prefetch depth (mainloop_reg)
+  using L = Slice<64>;
+  static constexpr int NW = WM * WN, THREADS = 64 * NW;  // 4 or 8 wavefronts
   static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
   static constexpr int FM = TM / 32, FN = TN / 32;  // 32x32 blocks per wave
-  static constexpr int ROWS = BM + BN;              // A rows then W rows in a stage
-  static constexpr int STAGE = ROWS * BK;           // halves per stage
-  static constexpr int LPT = ROWS / (4 * L::RPI);   // global_load_lds per thread per stage
-  static constexpr int OUT_LD = BN + 8;             // padded row of the fp16 output tile
-  static constexpr size_t RING = (size_t)STAGES * STAGE * sizeof(f16);
-  static constexpr size_t OUT = (size_t)BM * OUT_LD * sizeof(f16) + 8 * BM * sizeof(float);
+  static constexpr int LA = BM / (8 * NW), LW = BN / (8 * NW);  // copies per thread per slice
+  static constexpr int A_STAGE = BM * BK, W_STAGE = BN * BK;  // halves per slice
+  static constexpr int W_BASE = SA * A_STAGE;                 // W ring follows the A ring
+  static constexpr int OUT_LD = BN + 8;                       // padded row of the fp16 output tile
+  static constexpr int CA = BM * 8 / THREADS, CW = BN * 8 / THREADS;  // 16-B chunks per thread
+  static constexpr size_t RING = PD > 0 ? (size_t)2 * (A_STAGE + W_STAGE) * sizeof(f16)
+                                        : (size_t)(SA * A_STAGE + SW * W_STAGE) * sizeof(f16);
+  static constexpr size_t RED = 2 * WN * BM * sizeof(float);  // LayerNorm row partials
+  // The fp16 output tile is staged through LDS in NPASS row passes (one per
+  // wave row when the whole tile does not fit next to the partials).
+  static constexpr int NPASS = ((size_t)BM * OUT_LD * sizeof(f16) + RED <= kLdsMax) ? 1 : WM;
+  static constexpr size_t OUT = (size_t)(BM / NPASS) * OUT_LD * sizeof(f16) + RED;
   static constexpr size_t LDS = RING > OUT ? RING : OUT;
-  static_assert(WM * WN == 4, "four wavefronts");
+  static_assert(NW == 4 || NW == 8, "four or eight wavefronts");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is whole 32x32 blocks");
-  static_assert(ROWS % (4 * L::RPI) == 0 && BM % L::RPI == 0, "load distribution");
-  static_assert(STAGES >= 2, "pipeline depth");
-  static_assert(LPT * (STAGES - 2) < 64, "vmcnt range");
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load distribution");
+  static_assert(SA >= 2 && LA < 64, "A ring depth / vmcnt range");
+  static_assert(LDS <= kLdsMax, "LDS");
+  static_assert(PD == 0 || (BM * 8 % THREADS == 0 && BN * 8 % THREADS == 0), "chunks");
 };
 
-// Issue the global -> LDS copies of one K slice.  Each wavefront instruction
-// fills 1 KB = RPI rows; lane i lands at row i / CPR, slot i % CPR of them.
-template <class C>
-__device__ __forceinline__ void issue_slice(const f16* __restrict__ A, const f16* __restrict__ W,
-                                            int M, int K, int m0, int n0, int k0, f16* buf) {
-  using L = typename C::L;
+// Copy one 64-wide K slice of ROWS K-contiguous rows into LDS.  Each
+// wavefront instruction fills 1 KB = 8 rows; lane i lands at row i / 8, slot
+// i % 8 of them, so it fetches the logical chunk that belongs in that slot.
+// Rows at or past `valid` are read clamped to row valid-1.
+template <int ROWS, int NW>
+__device__ __forceinline__ void issue_rows(const f16* __restrict__ src, int ld, int valid,
+                                           f16* buf) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < C::LPT; ++j) {
-    const int g = wave * C::LPT + j;  // RPI-row group
-    const int r = g * L::RPI + lane / L::CPR;
-    const int sl = lane % L::CPR;
-    const int cl = sl ^ L::f(r);  // logical chunk that belongs in slot sl
-    const f16* src = (r < C::BM) ? A + (size_t)min(m0 + r, M - 1) * K + k0 + cl * 8
-                                 : W + (size_t)(n0 + r - C::BM) * K + k0 + cl * 8;
-    __builtin_amdgcn_global_load_lds(
-        src, (__attribute__((address_space(3))) void*)(buf + g * L::RPI * C::BK), 16, 0, 0);
+  for (int j = 0; j < ROWS / (8 * NW); ++j) {
+    const int g = wave * (ROWS / (8 * NW)) + j;  // 8-row group
+    const int r = g * 8 + (lane >> 3);
+    const int cl = (lane & 7) ^ Slice<64>::f(r);
+    __builtin_amdgcn_global_load_lds(src + (size_t)min(r, valid - 1) * ld + cl * 8,
+                                     (__attribute__((address_space(3))) void*)(buf + g * 8 * 64),
+                                     16, 0, 0);
   }
-}
-
-template <class C>
-__device__ __forceinline__ void wait_slices(int pending) {
-  // pending = slices allowed to stay in flight (0 .. STAGES-2)
-  if constexpr (C::STAGES >= 4) {
-    if (pending >= 2) { wait_vm<C::LPT * 2>(); return; }
-  }
-  if constexpr (C::STAGES >= 3) {
-    if (pending >= 1) { wait_vm<C::LPT>(); return; }
-  }
-  wait_vm<0>();
 }
 
 // Scheduling groups: (one DS read, then ~Q/R MFMAs) x R.
@@ -136,16 +120,57 @@ __device__ __forceinline__ void interleave() {
   }
 }
 
-// The K loop.  On return acc[fm][fn][i] = D(n, m) with
+// MFMA work of one 64-wide K slice staged in LDS (sA: BM rows, sW: BN rows).
+// Fragments are double-buffered across the four 16-wide k-steps and the
+// next step's LDS reads are spread over the current step's MFMAs.
+template <class C>
+__device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
+                                              f32x16 (&acc)[C::FM][C::FN]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int r32 = lane & 31, kh = lane >> 5;
+  constexpr int KS = C::BK / 16;    // MFMA k-steps per slice
+  constexpr int R = C::FM + C::FN;  // LDS fragment reads per k-step
+  constexpr int Q = C::FM * C::FN;  // MFMAs per k-step
+  f16x8 a[2][C::FM], w[2][C::FN];
+  auto rd = [&](int s, f16x8(&aa)[C::FM], f16x8(&ww)[C::FN]) {
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm)
+      aa[fm] = *reinterpret_cast<const f16x8*>(sA + C::L::off(wm * C::TM + fm * 32 + r32, 2 * s + kh));
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+      ww[fn] = *reinterpret_cast<const f16x8*>(sW + C::L::off(wn * C::TN + fn * 32 + r32, 2 * s + kh));
+  };
+  rd(0, a[0], w[0]);
+  __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // all of step 0's reads first
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (s + 1 < KS) rd(s + 1, a[(s + 1) & 1], w[(s + 1) & 1]);
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < C::FN; ++fn)
+        acc[fm][fn] = mfma32(w[s & 1][fn], a[s & 1][fm], acc[fm][fn]);
+    if (s + 1 < KS)
+      interleave<R, Q>();  // spread the next step's R fragment reads over these Q MFMAs
+    else
+      __builtin_amdgcn_sched_group_barrier(0x008, Q, 0);
+  }
+}
+
+// The K loop.  A (activations, streamed from HBM) and W (weights, L2
+// resident) have separate LDS rings: A runs SA-1 slices ahead, W one slice
+// ahead.  Iteration j issues W(j+1) and then A(j+SA-1); because the DMA
+// counter retires in issue order, waiting for W(kt) only has to allow the
+// LA copies of A(kt+SA-2) issued right after it to stay in flight, and A(kt)
+// (issued at j <= kt-2) is then complete too.
+// On return acc[fm][fn][i] = D(n, m) with
 //   n = n0 + wn*TN + fn*32 + 8*(i/4) + 4*(lane/32) + i%4,
 //   m = m0 + wm*TM + fm*32 + lane%32.
 template <class C>
 __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* __restrict__ W,
                                          int M, int K, int m0, int n0, f16* smem,
                                          f32x16 (&acc)[C::FM][C::FN]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / C::WN, wn = wave % C::WN;
-  const int r32 = lane & 31, kh = lane >> 5;
 #pragma unroll
   for (int fm = 0; fm < C::FM; ++fm)
 #pragma unroll
@@ -154,47 +179,101 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
       for (int i = 0; i < 16; ++i) acc[fm][fn][i] = 0.f;
 
   const int KT = K / C::BK;
+  f16* ringA = smem;
+  f16* ringW = smem + C::W_BASE;
+  const f16* a0 = A + (size_t)m0 * K;
+  const f16* w0 = W + (size_t)n0 * K;
+  auto issueA = [&](int s) {
+    issue_rows<C::BM, C::NW>(a0 + s * C::BK, K, M - m0, ringA + (s % C::SA) * C::A_STAGE);
+  };
+  auto issueW = [&](int s) {
+    issue_rows<C::BN, C::NW>(w0 + s * C::BK, K, C::BN, ringW + (s & 1) * C::W_STAGE);
+  };
+  // prologue = iterations j = -(SA-1) .. -1 of the same schedule
 #pragma unroll
-  for (int s = 0; s < C::STAGES - 1; ++s)
-    if (s < KT) issue_slice<C>(A, W, M, K, m0, n0, s * C::BK, smem + s * C::STAGE);
+  for (int j = 1 - C::SA; j <= -1; ++j) {
+    if (j == -1) issueW(0);
+    if (j + C::SA - 1 < KT) issueA(j + C::SA - 1);
+  }
 
-  constexpr int KS = C::BK / 16;         // MFMA k-steps per slice
-  constexpr int R = C::FM + C::FN;       // LDS fragment reads per k-step
-  constexpr int Q = C::FM * C::FN;       // MFMAs per k-step
   for (int kt = 0; kt < KT; ++kt) {
-    wait_slices<C>(min(C::STAGES - 2, KT - 1 - kt));
+    if (C::SA >= 3 && kt + C::SA - 2 < KT)
+      wait_vm<C::LA>();
+    else
+      wait_vm<0>();
     __syncthreads();  // slice kt visible to all; slice kt-1 fully consumed
-    const int nxt = kt + C::STAGES - 1;
-    if (nxt < KT)
-      issue_slice<C>(A, W, M, K, m0, n0, nxt * C::BK, smem + (nxt % C::STAGES) * C::STAGE);
-    const f16* sA = smem + (kt % C::STAGES) * C::STAGE;
-    const f16* sW = sA + C::BM * C::BK;
-    f16x8 a[2][C::FM], w[2][C::FN];
-    auto rd = [&](int s, f16x8(&aa)[C::FM], f16x8(&ww)[C::FN]) {
-#pragma unroll
-      for (int fm = 0; fm < C::FM; ++fm)
-        aa[fm] = *reinterpret_cast<const f16x8*>(sA + C::L::off(wm * C::TM + fm * 32 + r32, 2 * s + kh));
-#pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn)
-        ww[fn] = *reinterpret_cast<const f16x8*>(sW + C::L::off(wn * C::TN + fn * 32 + r32, 2 * s + kh));
-    };
-    rd(0, a[0], w[0]);
-    __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // all of step 0's reads first
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      if (s + 1 < KS) rd(s + 1, a[(s + 1) & 1], w[(s + 1) & 1]);
-#pragma unroll
-      for (int fm = 0; fm < C::FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < C::FN; ++fn)
-          acc[fm][fn] = mfma32(w[s & 1][fn], a[s & 1][fm], acc[fm][fn]);
-      if (s + 1 < KS)
-        interleave<R, Q>();  // spread the next step's R fragment reads over these Q MFMAs
-      else
-        __builtin_amdgcn_sched_group_barrier(0x008, Q, 0);
-    }
+    if (kt + 1 < KT) issueW(kt + 1);
+    if (kt + C::SA - 1 < KT) issueA(kt + C::SA - 1);
+    const f16* sA = ringA + (kt % C::SA) * C::A_STAGE;
+    const f16* sW = ringW + (kt & 1) * C::W_STAGE;
+    compute_slice<C>(sA, sW, acc);
   }
   __syncthreads();  // ring free for the epilogue
+}
+
+// The K loop with register staging: each thread keeps the 16-byte chunks of
+// the next PD slices in flight in VGPRs (the register file holds far more
+// in-flight bytes than LDS), then writes one slice per iteration into a
+// double-buffered LDS tile.  The compiler's own counters order the register
+// loads; buffer kt&1 was last read in iteration kt-2, before barrier kt-1.
+template <class C>
+__device__ __forceinline__ void mainloop_reg(const f16* __restrict__ A,
+                                             const f16* __restrict__ W, int M, int K, int m0,
+                                             int n0, f16* smem, f32x16 (&acc)[C::FM][C::FN]) {
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[fm][fn][i] = 0.f;
+  constexpr int D = C::PD, CA = C::CA, CW = C::CW;
+  const int KT = K / C::BK, tid = threadIdx.x, last = M - m0 - 1;
+  const f16* a0 = A + (size_t)m0 * K;
+  const f16* w0 = W + (size_t)n0 * K;
+  f16x8 ra[D][CA], rw[D][CW];
+  auto load = [&](int s, f16x8(&xa)[CA], f16x8(&xw)[CW]) {
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int c = tid + i * C::THREADS, r = c >> 3;
+      xa[i] = *reinterpret_cast<const f16x8*>(a0 + (size_t)min(r, last) * K + s * C::BK + (c & 7) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+      const int c = tid + i * C::THREADS, r = c >> 3;
+      xw[i] = *reinterpret_cast<const f16x8*>(w0 + (size_t)r * K + s * C::BK + (c & 7) * 8);
+    }
+  };
+  auto store = [&](int buf, const f16x8(&xa)[CA], const f16x8(&xw)[CW]) {
+    f16* sA = smem + buf * (C::A_STAGE + C::W_STAGE);
+    f16* sW = sA + C::A_STAGE;
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+      const int c = tid + i * C::THREADS;
+      *reinterpret_cast<f16x8*>(sA + C::L::off(c >> 3, c & 7)) = xa[i];
+    }
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+      const int c = tid + i * C::THREADS;
+      *reinterpret_cast<f16x8*>(sW + C::L::off(c >> 3, c & 7)) = xw[i];
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < KT) load(d, ra[d], rw[d]);
+  for (int kt0 = 0; kt0 < KT; kt0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int kt = kt0 + d;
+      if (kt < KT) {
+        store(kt & 1, ra[d], rw[d]);
+        if (kt + D < KT) load(kt + D, ra[d], rw[d]);
+        __syncthreads();
+        const f16* sA = smem + (kt & 1) * (C::A_STAGE + C::W_STAGE);
+        compute_slice<C>(sA, sA + C::A_STAGE, acc);
+      }
+    }
+  }
+  __syncthreads();  // LDS free for the epilogue
 }
 
 // Tile coordinates from the workgroup id, XCD-aware (see header).
@@ -205,12 +284,13 @@ __device__ __forceinline__ bool tile_of(int nb, int mb, int& mi, int& ni) {
   return mi < mb;
 }
 
-// Write the fp16 tile staged in LDS (BM x OUT_LD) to C with 16-byte stores.
-template <class C>
-__device__ __forceinline__ void store_tile(const f16* tile, f16* __restrict__ out, int ldc, int M,
+// Write ROWS rows of the output tile, staged in LDS as ROWS x OUT_LD fp16,
+// to C rows m0.. with 16-byte stores.
+template <class C, int ROWS>
+__device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ out, int ldc, int M,
                                            int m0, int n0) {
   constexpr int CPR = C::BN / 8;
-  for (int idx = threadIdx.x; idx < C::BM * CPR; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < ROWS * CPR; idx += C::THREADS) {
     const int r = idx / CPR, c = idx % CPR;
     if (m0 + r < M)
       *reinterpret_cast<f16x8*>(out + (size_t)(m0 + r) * ldc + n0 + c * 8) =
@@ -219,7 +299,7 @@ __device__ __forceinline__ void store_tile(const f16* tile, f16* __restrict__ ou
 }
 
 template <class C, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(
+__global__ __launch_bounds__(C::THREADS) void gemm_kernel(
     const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
     const f16* residual, const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* out,
     int M, int N, int K, float eps) {
@@ -228,47 +308,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
   if (!tile_of(N / C::BN, (M + C::BM - 1) / C::BM, mi, ni)) return;
   const int m0 = mi * C::BM, n0 = ni * C::BN;
   f32x16 acc[C::FM][C::FN];
-  mainloop<C>(A, W, M, K, m0, n0, smem, acc);
+  if constexpr (C::PD > 0)
+    mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
+  else
+    mainloop<C>(A, W, M, K, m0, n0, smem, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int r32 = lane & 31, kh = lane >> 5;
-  f16* tile = smem;  // BM x OUT_LD fp16
-  float* red = reinterpret_cast<float*>(smem + C::BM * C::OUT_LD);  // [2][4][BM]
+  constexpr int PR = C::BM / C::NPASS;  // tile rows staged per pass
+  f16* tile = smem;                     // PR x OUT_LD fp16
+  float* red = reinterpret_cast<float*>(smem + PR * C::OUT_LD);  // [2][WN][BM]
+  float mean[C::FM], rstd[C::FM];
 
-  if constexpr (EPI != kLayerNorm) {
-    // One 32x32 block at a time (bias, + GELU or + residual, to fp16 in LDS);
-    // the scheduling fence keeps a single block's values live.
+  if constexpr (EPI == kLayerNorm) {
+    static_assert(C::BN == kHidden, "LayerNorm tile owns whole 384-wide rows");
+    // v = acc + bias + residual, then two-pass row statistics: per-lane sums,
+    // lane ^ 32 holds the other half of the wave's columns, LDS across wn.
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
-      const int ml = wm * C::TM + fm * 32 + r32;  // row inside the tile
-      const int mg = min(m0 + ml, M - 1);
-#pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
-          const f16x4 bv = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
-          f16x4 rv = {0, 0, 0, 0};
-          if (EPI == kResidual) rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * N + n0 + nl);
-          f16x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = acc[fm][fn][4 * j + i] + (float)bv[i] + (float)rv[i];
-            if (EPI == kGelu) v = gelu_as(v);
-            o[i] = (f16)v;
-          }
-          *reinterpret_cast<f16x4*>(tile + ml * C::OUT_LD + nl) = o;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  } else {
-    static_assert(C::BN == kHidden && C::WM == 1, "LayerNorm tile owns whole rows");
-    // v = acc + bias + residual
-#pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
-      const int mg = min(m0 + fm * 32 + r32, M - 1);
+      const int mg = min(m0 + wm * C::TM + fm * 32 + r32, M - 1);
 #pragma unroll
       for (int fn = 0; fn < C::FN; ++fn)
 #pragma unroll
@@ -280,7 +339,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
           for (int i = 0; i < 4; ++i) acc[fm][fn][4 * j + i] += (float)bv[i] + (float)rv[i];
         }
     }
-    float mean[C::FM], rstd[C::FM];
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
       float s = 0.f;
@@ -289,14 +347,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) s += acc[fm][fn][i];
       s += __shfl_xor(s, 32, kWave);
-      if (kh == 0) red[wave * C::BM + fm * 32 + r32] = s;
+      if (kh == 0) red[wn * C::BM + wm * C::TM + fm * 32 + r32] = s;
     }
     __syncthreads();
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
-      const int row = fm * 32 + r32;
-      mean[fm] = (red[row] + red[C::BM + row] + red[2 * C::BM + row] + red[3 * C::BM + row]) *
-                 (1.0f / kHidden);
+      const int row = wm * C::TM + fm * 32 + r32;
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < C::WN; ++w) t += red[w * C::BM + row];
+      mean[fm] = t * (1.0f / kHidden);
       float q = 0.f;
 #pragma unroll
       for (int fn = 0; fn < C::FN; ++fn)
@@ -306,39 +366,65 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(
           q += d * d;
         }
       q += __shfl_xor(q, 32, kWave);
-      if (kh == 0) red[4 * C::BM + wave * C::BM + row] = q;
+      if (kh == 0) red[(C::WN + wn) * C::BM + row] = q;
     }
     __syncthreads();
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
-      const int row = fm * 32 + r32;
-      const float var = (red[4 * C::BM + row] + red[5 * C::BM + row] + red[6 * C::BM + row] +
-                         red[7 * C::BM + row]) *
-                        (1.0f / kHidden);
-      rstd[fm] = rsqrtf(var + eps);
-    }
+      const int row = wm * C::TM + fm * 32 + r32;
+      float t = 0.f;
 #pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
-      const int ml = fm * 32 + r32;
-#pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
-          const f16x4 gv = *reinterpret_cast<const f16x4*>(gamma + nl);
-          const f16x4 bv = *reinterpret_cast<const f16x4*>(beta + nl);
-          f16x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] * (float)gv[i] + (float)bv[i]);
-          *reinterpret_cast<f16x4*>(tile + ml * C::OUT_LD + nl) = o;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int w = 0; w < C::WN; ++w) t += red[(C::WN + w) * C::BM + row];
+      rstd[fm] = rsqrtf(t * (1.0f / kHidden) + eps);
     }
   }
-  __syncthreads();
-  store_tile<C>(tile, out, N, M, m0, n0);
+
+  // fp16 tile into LDS (row pass p holds tile rows [p*PR, (p+1)*PR)), then
+  // coalesced stores.  One 32x32 block at a time; the scheduling fence keeps
+  // a single block's values live.
+#pragma unroll
+  for (int p = 0; p < C::NPASS; ++p) {
+    if (C::NPASS == 1 || wm == p) {
+#pragma unroll
+      for (int fm = 0; fm < C::FM; ++fm) {
+        const int ml = wm * C::TM + fm * 32 + r32;  // row inside the tile
+        const int mg = min(m0 + ml, M - 1);
+#pragma unroll
+        for (int fn = 0; fn < C::FN; ++fn) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
+            f16x4 o;
+            if constexpr (EPI == kLayerNorm) {
+              const f16x4 gv = *reinterpret_cast<const f16x4*>(gamma + nl);
+              const f16x4 bv = *reinterpret_cast<const f16x4*>(beta + nl);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] * (float)gv[i] +
+                             (float)bv[i]);
+            } else {
+              const f16x4 bv =
+                  bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
+              f16x4 rv = {0, 0, 0, 0};
+              if (EPI == kResidual)
+                rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * N + n0 + nl);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float v = acc[fm][fn][4 * j + i] + (float)bv[i] + (float)rv[i];
+                if (EPI == kGelu) v = gelu_as(v);
+                o[i] = (f16)v;
+              }
+            }
+            *reinterpret_cast<f16x4*>(tile + (ml - p * PR) * C::OUT_LD + nl) = o;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    __syncthreads();
+    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0);
+    if (p + 1 < C::NPASS) __syncthreads();
+  }
 }
 
 // Any-shape fallback (the role of src/kernels/matmul.cu:34-59): 16x16 output
@@ -371,7 +457,7 @@ template <class C, int EPI>
 hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residual,
                   const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
                   hipStream_t s) {
-  if constexpr (EPI == kLayerNorm && (C::BN != kHidden || C::WM != 1)) {
+  if constexpr (EPI == kLayerNorm && C::BN != kHidden) {
     return hipErrorInvalidValue;  // LayerNorm needs a tile that owns whole rows
   } else {
     if (N % C::BN != 0) return hipErrorInvalidValue;
@@ -381,58 +467,86 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
     if (attr != hipSuccess) return attr;
     const int nb = N / C::BN, mb = (M + C::BM - 1) / C::BM;
     const int grid = nb * 8 * ((mb + 7) / 8);
-    hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(kThreads), C::LDS, s, A, W, bias,
+    hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(C::THREADS), C::LDS, s, A, W, bias,
                        residual, gamma, beta, out, M, N, K, eps);
     return hipGetLastError();
   }
 }
 
-// Tile configurations (BM, BN, wavefronts M x N, pipeline stages, K slice),
-// by id.
-//   id  tile      wave tile  stages x BK   LDS
-//    0  64x64     32x32      4 x 64         64 KB
-//    1  64x128    32x64      4 x 64         96 KB
-//    2  128x64    64x32      4 x 64         96 KB
-//    3  128x128   64x64      3 x 64         96 KB
-//    4  256x128   128x64     2 x 64         96 KB
-//    5  128x384   128x96     2 x 64        128 KB   (owns whole 384-wide rows)
-//    6  64x384    64x96      2 x 64        112 KB   (owns whole rows)
-//    7  32x128    32x32      4 x 64         80 KB
-//    8  128x192   64x96      3 x 64        120 KB
-//    9  256x192   128x96     2 x 64        112 KB
-//   10  32x384    32x96      3 x 64        156 KB   (owns whole rows)
-//   11  128x384   128x96     4 x 32        128 KB   (owns whole rows)
-//   12  256x192   128x96     4 x 32        112 KB
-//   13  128x192   64x96      4 x 32         80 KB
-//   14  64x384    64x96      4 x 32        112 KB   (owns whole rows)
-//   15  256x128   128x64     4 x 32         96 KB
-//   16  128x128   64x64      6 x 32         96 KB
+// Tile configurations (BM, BN, wavefronts M x N, A-ring depth), by id; the K
+// slice is 64 wide and the W ring 2 deep throughout.
+//   id  tile      wave tile  SA   LDS
+//    0  64x64     32x32      4    48 KB
+//    1  64x128    32x64      4    64 KB
+//    2  128x64    64x32      4    80 KB
+//    3  128x128   64x64      4    96 KB
+//    4  256x128   128x64     3   128 KB
+//    5  128x384   128x96     4   160 KB   (owns whole 384-wide rows)
+//    6  64x384    64x96      4   128 KB   (owns whole rows)
+//    7  32x128    32x32      4    48 KB
+//    8  128x192   64x96      4   112 KB
+//    9  256x192   128x96     3   144 KB
+//   10  32x384    32x96      4   112 KB   (owns whole rows)
+//   11  128x384   128x96     3   144 KB   (owns whole rows)
+//   12  256x192   128x96     2   112 KB
+//   13  128x192   64x96      3    96 KB
+//   14  64x384    64x96      2   112 KB   (owns whole rows)
+//   15  128x128   64x64      2    64 KB
+//   16  64x128    32x64      6    80 KB
+//   8 wavefronts (2 per SIMD):
+//   17  256x384   128x96     2   160 KB   (owns whole rows)
+//   18  128x384   64x96      4   160 KB   (owns whole rows)
+//   19  256x192   64x96      3   144 KB
+//   20  256x128   64x64      3   128 KB
+//   21  128x256   64x64      4   128 KB
+//   register-staged K slices (PD slices in flight in VGPRs, LDS double buffer):
+//   22  128x128   64x64      PD 3   64 KB
+//   23  128x128   64x64      PD 4   64 KB
+//   24  128x256   64x64 (8w) PD 2   96 KB
+//   25  256x128   64x64 (8w) PD 2   96 KB
+//   26  64x64     32x32      PD 4   32 KB
+//   27  128x192   64x96      PD 3   80 KB
+//   28  128x384   64x96 (8w) PD 2  128 KB   (owns whole rows)
+//   29  256x128   128x64     PD 3   96 KB
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
                      const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
                      hipStream_t s) {
-#define BBH_CFG(ID, BM, BN, WM, WN, ST, BKV)                                                    \
+#define BBH_CFG(ID, BM, BN, WM, WN, SA, ...)                                                        \
   case ID:                                                                                    \
-    return launch<Cfg<BM, BN, WM, WN, ST, BKV>, EPI>(A, W, bias, residual, gamma, beta, out, M, \
-                                                     N, K, eps, s);
+    return launch<Cfg<BM, BN, WM, WN, SA, ##__VA_ARGS__>, EPI>(A, W, bias, residual, gamma, beta, out, M, N, \
+                                                K, eps, s);
   switch (id) {
-    BBH_CFG(0, 64, 64, 2, 2, 4, 64)
-    BBH_CFG(1, 64, 128, 2, 2, 4, 64)
-    BBH_CFG(2, 128, 64, 2, 2, 4, 64)
-    BBH_CFG(3, 128, 128, 2, 2, 3, 64)
-    BBH_CFG(4, 256, 128, 2, 2, 2, 64)
-    BBH_CFG(5, 128, 384, 1, 4, 2, 64)
-    BBH_CFG(6, 64, 384, 1, 4, 2, 64)
-    BBH_CFG(7, 32, 128, 1, 4, 4, 64)
-    BBH_CFG(8, 128, 192, 2, 2, 3, 64)
-    BBH_CFG(9, 256, 192, 2, 2, 2, 64)
-    BBH_CFG(10, 32, 384, 1, 4, 3, 64)
-    BBH_CFG(11, 128, 384, 1, 4, 4, 32)
-    BBH_CFG(12, 256, 192, 2, 2, 4, 32)
-    BBH_CFG(13, 128, 192, 2, 2, 4, 32)
-    BBH_CFG(14, 64, 384, 1, 4, 4, 32)
-    BBH_CFG(15, 256, 128, 2, 2, 4, 32)
-    BBH_CFG(16, 128, 128, 2, 2, 6, 32)
+    BBH_CFG(0, 64, 64, 2, 2, 4)
+    BBH_CFG(1, 64, 128, 2, 2, 4)
+    BBH_CFG(2, 128, 64, 2, 2, 4)
+    BBH_CFG(3, 128, 128, 2, 2, 4)
+    BBH_CFG(4, 256, 128, 2, 2, 3)
+    BBH_CFG(5, 128, 384, 1, 4, 4)
+    BBH_CFG(6, 64, 384, 1, 4, 4)
+    BBH_CFG(7, 32, 128, 1, 4, 4)
+    BBH_CFG(8, 128, 192, 2, 2, 4)
+    BBH_CFG(9, 256, 192, 2, 2, 3)
+    BBH_CFG(10, 32, 384, 1, 4, 4)
+    BBH_CFG(11, 128, 384, 1, 4, 3)
+    BBH_CFG(12, 256, 192, 2, 2, 2)
+    BBH_CFG(13, 128, 192, 2, 2, 3)
+    BBH_CFG(14, 64, 384, 1, 4, 2)
+    BBH_CFG(15, 128, 128, 2, 2, 2)
+    BBH_CFG(16, 64, 128, 2, 2, 6)
+    BBH_CFG(17, 256, 384, 2, 4, 2)
+    BBH_CFG(18, 128, 384, 2, 4, 4)
+    BBH_CFG(19, 256, 192, 4, 2, 3)
+    BBH_CFG(20, 256, 128, 4, 2, 3)
+    BBH_CFG(21, 128, 256, 2, 4, 4)
+    BBH_CFG(22, 128, 128, 2, 2, 2, 3)
+    BBH_CFG(23, 128, 128, 2, 2, 2, 4)
+    BBH_CFG(24, 128, 256, 2, 4, 2, 2)
+    BBH_CFG(25, 256, 128, 4, 2, 2, 2)
+    BBH_CFG(26, 64, 64, 2, 2, 2, 4)
+    BBH_CFG(27, 128, 192, 2, 2, 2, 3)
+    BBH_CFG(28, 128, 384, 2, 4, 2, 2)
+    BBH_CFG(29, 256, 128, 2, 2, 2, 3)
   }
 #undef BBH_CFG
   return hipErrorInvalidValue;
@@ -440,16 +554,27 @@ hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const 
 
 // Tile choice per shape, from sweeps of every id at the path's shapes on
 // MI355X (M = 2048..8192 for the varlen batches, 131072 for batch 256 x 512).
-constexpr int kBnOf[] = {64, 128, 64, 128, 128, 384, 384, 128, 192, 192, 384, 384, 192, 192, 384, 128, 128};
+constexpr int kBnOf[] = {64,  128, 64,  128, 128, 384, 384, 128, 192, 192, 384,
+                         384, 192, 192, 384, 128, 128, 384, 384, 192, 128, 256,
+                         128, 128, 256, 128, 64,  192, 384, 128};
 
-int pick_plain(int M, int N) {
+// Tile config per shape, from sweeps on MI355X over the encoder's four
+// shapes (N, K) = (1152, 384) QKV, (1536, 384) FFN1, (384, 384) O-proj and
+// (384, 1536) FFN2.  Small M wants many small tiles (latency, CU coverage);
+// large M wants big tiles (L2 and LDS traffic per MFMA).
+int pick_plain(int M, int N, int K) {
+  const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
-  if (M >= 16384)
-    id = (N == 1152) ? 9 : 13;
-  else if (M > 4096)
-    id = (N == 1152) ? 9 : (N == 384 ? 3 : 0);
+  if (M <= 4096)
+    id = (qkv && M > 2048) ? 16 : 26;
+  else if (M <= 12288)
+    id = qkv ? 18 : ffn1 ? 26 : 0;
+  else if (M <= 24576)
+    id = qkv ? 22 : ffn1 ? 15 : wide_k ? 15 : 26;
+  else if (M < 98304)
+    id = qkv ? 19 : ffn1 ? 23 : wide_k ? 19 : 22;
   else
-    id = (N == 1152) ? 3 : 0;
+    id = qkv ? 18 : ffn1 ? 23 : wide_k ? 17 : 19;
   return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
 }
 
@@ -468,7 +593,7 @@ hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int 
                        gelu ? 1 : 0);
     return hipGetLastError();
   }
-  const int id = pick_plain(M, N);
+  const int id = pick_plain(M, N, K);
   return gelu ? launch_id<kGelu>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s)
               : launch_id<kBias>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s);
 }
@@ -480,9 +605,9 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f
   // tile that owns whole rows leaves most CUs idle and streams all of W per
   // workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
   // (in place over y) and the row LayerNorm follows as its own pass.
-  if (M >= 16384)
-    return launch_id<kLayerNorm>(5, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
-  hipError_t e = launch_id<kResidual>(pick_plain(M, kHidden), A, W, bias, residual, nullptr,
+  if (M > 24576)
+    return launch_id<kLayerNorm>(18, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
+  hipError_t e = launch_id<kResidual>(pick_plain(M, kHidden, K), A, W, bias, residual, nullptr,
                                       nullptr, y, M, kHidden, K, eps, s);
   if (e != hipSuccess) return e;
   return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);

@@ -16,6 +16,19 @@ c_int, c_float, c_size_t, c_void_p, c_char_p = (ctypes.c_int, ctypes.c_float, ct
                                                ctypes.c_void_p, ctypes.c_char_p)
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 
+
+class AttnWeights(ctypes.Structure):
+    """bbh_attn_weights: device pointers of one layer's attention tensors."""
+    _fields_ = [(n, c_void_p) for n in ("qkv_w", "qkv_b", "o_w", "o_b", "ln_w", "ln_b")]
+
+
+class FfnWeights(ctypes.Structure):
+    """bbh_ffn_weights: device pointers of one layer's feed-forward tensors."""
+    _fields_ = [(n, c_void_p) for n in ("inter_w", "inter_b", "out_w", "out_b", "ln_w", "ln_b")]
+
+
+_AWp, _FWp = ctypes.POINTER(AttnWeights), ctypes.POINTER(FfnWeights)
+
 # name -> (restype, argtypes); every symbol declared in include/bbh.h.
 SIGNATURES = {
     "bbh_status_string": (c_char_p, [c_int]),
@@ -40,6 +53,12 @@ SIGNATURES = {
     "bbh_pool_free": (c_int, [c_void_p]),
     "bbh_embed_batches": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "bbh_model_layer": (c_int, [c_void_p, c_int, _AWp, _FWp]),
+    "bbh_attention_block_w": (c_int, [c_void_p, c_void_p, _AWp, c_void_p, c_void_p, c_int, c_int,
+                                      c_void_p]),
+    "bbh_ffn_block_w": (c_int, [c_void_p, c_void_p, _FWp, c_void_p, c_int, c_int, c_void_p]),
+    "bbh_encoder_layer_w": (c_int, [c_void_p, c_void_p, _AWp, _FWp, c_void_p, c_void_p, c_int, c_int,
+                                    c_void_p]),
     "bbh_attention_block": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int,
                                     c_int, c_void_p]),
     "bbh_ffn_block": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_void_p]),
@@ -63,6 +82,7 @@ SIGNATURES = {
     "bbh_mean_pool": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "bbh_l2_normalize": (c_int, [c_void_p, c_int, c_int, c_void_p]),
     "bbh_pool_normalize": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "bbh_gelu": (c_int, [c_void_p, c_int, c_void_p]),
 }
 
 STATUS = {

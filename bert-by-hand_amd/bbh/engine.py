@@ -307,6 +307,11 @@ def launch_l2_normalize(x, n, batch=1, stream=None):
     return x
 
 
+def launch_gelu(x, n, stream=None):
+    call("bbh_gelu", _ptr(x), n, _stream(stream))
+    return x
+
+
 def launch_pool_normalize(hidden, mask, out, seq, batch=1, stream=None):
     call("bbh_pool_normalize", _ptr(hidden), _ptr(mask), _ptr(out), seq, HIDDEN, batch,
          _stream(stream))

@@ -545,7 +545,96 @@ static bbh_status check_layer(const bbh_workspace* ws, const bbh_model* m, int l
   if (layer < 0 || layer >= BBH_NUM_LAYERS)
     return fail(BBH_ERR_INVALID_ARG, "layer index " + std::to_string(layer) + " out of range");
   if (hidden == out) return fail(BBH_ERR_INVALID_ARG, "out may not alias hidden");
+  if (!aligned(hidden, 16) || !aligned(out, 16)) return misaligned("hidden/out");
   return check_shape(ws, batch, seq);
+}
+
+// Caller-held weight views -> the internal per-layer pointer set (only the
+// half a block reads is filled), with the alignment the kernels rely on.
+static bbh_status layer_from(const bbh_attn_weights* a, const bbh_ffn_weights* f,
+                             bbh_model::Layer* L) {
+  *L = {};
+  if (a) {
+    if (!a->qkv_w || !a->qkv_b || !a->o_w || !a->o_b || !a->ln_w || !a->ln_b)
+      return fail(BBH_ERR_INVALID_ARG, "null attention weight pointer");
+    if (!aligned(a->qkv_w, 16) || !aligned(a->o_w, 16) || !aligned(a->qkv_b, 8) ||
+        !aligned(a->o_b, 8) || !aligned(a->ln_w, 8) || !aligned(a->ln_b, 8))
+      return misaligned("attention weights");
+    L->qkv_w = static_cast<const f16*>(a->qkv_w);
+    L->qkv_b = static_cast<const f16*>(a->qkv_b);
+    L->o_w = static_cast<const f16*>(a->o_w);
+    L->o_b = static_cast<const f16*>(a->o_b);
+    L->ln1_g = static_cast<const f16*>(a->ln_w);
+    L->ln1_b = static_cast<const f16*>(a->ln_b);
+  }
+  if (f) {
+    if (!f->inter_w || !f->inter_b || !f->out_w || !f->out_b || !f->ln_w || !f->ln_b)
+      return fail(BBH_ERR_INVALID_ARG, "null ffn weight pointer");
+    if (!aligned(f->inter_w, 16) || !aligned(f->out_w, 16) || !aligned(f->inter_b, 8) ||
+        !aligned(f->out_b, 8) || !aligned(f->ln_w, 8) || !aligned(f->ln_b, 8))
+      return misaligned("ffn weights");
+    L->f1_w = static_cast<const f16*>(f->inter_w);
+    L->f1_b = static_cast<const f16*>(f->inter_b);
+    L->f2_w = static_cast<const f16*>(f->out_w);
+    L->f2_b = static_cast<const f16*>(f->out_b);
+    L->ln2_g = static_cast<const f16*>(f->ln_w);
+    L->ln2_b = static_cast<const f16*>(f->ln_b);
+  }
+  return BBH_OK;
+}
+
+static bbh_status check_block(const bbh_workspace* ws, const void* hidden, const void* out,
+                              int batch, int seq) {
+  if (!ws || !hidden || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  if (hidden == out) return fail(BBH_ERR_INVALID_ARG, "out may not alias hidden");
+  if (!aligned(hidden, 16) || !aligned(out, 16)) return misaligned("hidden/out");
+  return check_shape(ws, batch, seq);
+}
+
+bbh_status bbh_model_layer(const bbh_model* m, int layer, bbh_attn_weights* attn,
+                           bbh_ffn_weights* ffn) {
+  if (!m) return fail(BBH_ERR_INVALID_ARG, "null model");
+  if (layer < 0 || layer >= BBH_NUM_LAYERS)
+    return fail(BBH_ERR_INVALID_ARG, "layer index " + std::to_string(layer) + " out of range");
+  const bbh_model::Layer& L = m->layers[layer];
+  if (attn) *attn = {L.qkv_w, L.qkv_b, L.o_w, L.o_b, L.ln1_g, L.ln1_b};
+  if (ffn) *ffn = {L.f1_w, L.f1_b, L.f2_w, L.f2_b, L.ln2_g, L.ln2_b};
+  return BBH_OK;
+}
+
+bbh_status bbh_attention_block_w(bbh_workspace* ws, const void* hidden, const bbh_attn_weights* w,
+                                 const int32_t* mask, void* out, int batch, int seq,
+                                 bbh_stream_t stream) {
+  BBH_TRY(check_block(ws, hidden, out, batch, seq));
+  if (!w || !mask) return fail(BBH_ERR_INVALID_ARG, "null weights or mask");
+  bbh_model::Layer L;
+  BBH_TRY(layer_from(w, nullptr, &L));
+  return run_attention_block(ws, L, static_cast<const f16*>(hidden), mask, static_cast<f16*>(out),
+                             batch, seq, S(stream));
+}
+
+bbh_status bbh_ffn_block_w(bbh_workspace* ws, const void* hidden, const bbh_ffn_weights* w,
+                           void* out, int batch, int seq, bbh_stream_t stream) {
+  BBH_TRY(check_block(ws, hidden, out, batch, seq));
+  if (!w) return fail(BBH_ERR_INVALID_ARG, "null weights");
+  bbh_model::Layer L;
+  BBH_TRY(layer_from(nullptr, w, &L));
+  return run_ffn_block(ws, L, static_cast<const f16*>(hidden), static_cast<f16*>(out), batch, seq,
+                       S(stream));
+}
+
+bbh_status bbh_encoder_layer_w(bbh_workspace* ws, const void* hidden, const bbh_attn_weights* attn,
+                               const bbh_ffn_weights* ffn, const int32_t* mask, void* out,
+                               int batch, int seq, bbh_stream_t stream) {
+  BBH_TRY(check_block(ws, hidden, out, batch, seq));
+  if (!attn || !ffn || !mask) return fail(BBH_ERR_INVALID_ARG, "null weights or mask");
+  if (out == ws->attn_out) return fail(BBH_ERR_INVALID_ARG, "out may not be the workspace's attn_out");
+  bbh_model::Layer L;
+  BBH_TRY(layer_from(attn, ffn, &L));
+  const hipStream_t s = S(stream);
+  BBH_TRY(run_attention_block(ws, L, static_cast<const f16*>(hidden), mask, ws->attn_out, batch,
+                              seq, s));
+  return run_ffn_block(ws, L, ws->attn_out, static_cast<f16*>(out), batch, seq, s);
 }
 
 bbh_status bbh_attention_block(bbh_workspace* ws, const bbh_model* m, int layer,
@@ -724,6 +813,13 @@ bbh_status bbh_pool_normalize(const void* hidden, const int32_t* mask, void* out
   return check_launch(bbh::pool_normalize(static_cast<const f16*>(hidden), mask,
                                           static_cast<f16*>(out), batch, seq, S(stream)),
                       "pool+normalize");
+}
+
+bbh_status bbh_gelu(void* x, int n, bbh_stream_t stream) {
+  if (n < 0) return fail(BBH_ERR_INVALID_ARG, "bbh_gelu: n must be >= 0");
+  if (n == 0) return BBH_OK;
+  if (!x) return fail(BBH_ERR_INVALID_ARG, "bbh_gelu: null x");
+  return check_launch(bbh::gelu(static_cast<f16*>(x), (size_t)n, S(stream)), "gelu");
 }
 
 }  // extern "C"

@@ -57,4 +57,7 @@ hipError_t l2_normalize(f16* x, int n, int batch, hipStream_t s);
 hipError_t pool_normalize(const f16* hidden, const int32_t* mask, f16* out, int batch,
                           int seq, hipStream_t s);
 
+// Exact-erf GELU in place over n values.
+hipError_t gelu(f16* x, size_t n, hipStream_t s);
+
 }  // namespace bbh

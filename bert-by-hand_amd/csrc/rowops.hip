@@ -231,6 +231,23 @@ __global__ __launch_bounds__(256) void l2_normalize_kernel(f16* x, int n) {
   for (int i = threadIdx.x; i < n; i += 256) r[i] = (f16)((float)r[i] * inv);
 }
 
+// Exact GELU in place (src/kernels/gelu.h:5-9, gelu.cu): eight values per
+// thread with 16-byte accesses; the tail, or a buffer not 16-byte aligned,
+// one value per thread.
+__global__ __launch_bounds__(256) void gelu8_kernel(f16* x, size_t n8) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  f16x8 v = reinterpret_cast<f16x8*>(x)[i];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (f16)gelu_erf((float)v[j]);
+  reinterpret_cast<f16x8*>(x)[i] = v;
+}
+
+__global__ __launch_bounds__(256) void gelu1_kernel(f16* x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) x[i] = (f16)gelu_erf((float)x[i]);
+}
+
 }  // namespace
 
 hipError_t layernorm(const f16* x, const f16* residual, const f16* gamma, const f16* beta,
@@ -274,6 +291,17 @@ hipError_t mean_pool(const f16* hidden, const int32_t* mask, f16* out, int batch
 
 hipError_t l2_normalize(f16* x, int n, int batch, hipStream_t s) {
   hipLaunchKernelGGL(l2_normalize_kernel, dim3(batch), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
+hipError_t gelu(f16* x, size_t n, hipStream_t s) {
+  const size_t n8 = ((uintptr_t)x & 15) ? 0 : n / 8;
+  if (n8)
+    hipLaunchKernelGGL(gelu8_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, x, n8);
+  const size_t rest = n - n8 * 8;
+  if (rest)
+    hipLaunchKernelGGL(gelu1_kernel, dim3((unsigned)((rest + 255) / 256)), dim3(256), 0, s,
+                       x + n8 * 8, rest);
   return hipGetLastError();
 }
 

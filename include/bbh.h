@@ -140,9 +140,39 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
                              const int *seqs, const int64_t *emb_rows, void *emb,
                              int n_batches, bbh_stream_t stream);
 
+/* ---- weight views (src/model/encoder.h:11-22,37-40) -------------------------
+ * Device pointers of one encoder layer's fp16 tensors, the reference's
+ * AttnWeights / FfnWeights field for field.  Matrices must be 16-byte
+ * aligned and vectors 8-byte aligned (every hipMalloc'd buffer is). */
+typedef struct bbh_attn_weights {
+  const void *qkv_w, *qkv_b; /* (1152, 384) with Q|K|V row blocks, (1152) */
+  const void *o_w, *o_b;     /* attention output dense (384, 384), (384) */
+  const void *ln_w, *ln_b;   /* attention output LayerNorm (384), (384) */
+} bbh_attn_weights;
+typedef struct bbh_ffn_weights {
+  const void *inter_w, *inter_b; /* intermediate dense (1536, 384), (1536) */
+  const void *out_w, *out_b;     /* output dense (384, 1536), (384) */
+  const void *ln_w, *ln_b;       /* output LayerNorm (384), (384) */
+} bbh_ffn_weights;
+/* ModelWeights::layer(i) (src/model/weights.h:77-86): the views of encoder
+ * layer `layer` of a loaded model.  Either output may be NULL. */
+bbh_status bbh_model_layer(const bbh_model *m, int layer, bbh_attn_weights *attn,
+                           bbh_ffn_weights *ffn);
+
 /* ---- block level (src/model/encoder.h:27-46) ------------------------------
- * hidden / out: (batch*seq, 384) fp16, mask (batch, seq) int32; `layer`
- * selects the model's encoder layer.  out may not alias hidden. */
+ * hidden / out: (batch*seq, 384) fp16, 16-byte aligned; mask (batch, seq)
+ * int32.  out may not alias hidden.  The _w forms take the reference's
+ * weight views; the others select layer `layer` of a loaded model. */
+bbh_status bbh_attention_block_w(bbh_workspace *ws, const void *hidden,
+                                 const bbh_attn_weights *w, const int32_t *mask,
+                                 void *out, int batch, int seq, bbh_stream_t stream);
+bbh_status bbh_ffn_block_w(bbh_workspace *ws, const void *hidden,
+                           const bbh_ffn_weights *w, void *out, int batch, int seq,
+                           bbh_stream_t stream);
+bbh_status bbh_encoder_layer_w(bbh_workspace *ws, const void *hidden,
+                               const bbh_attn_weights *attn, const bbh_ffn_weights *ffn,
+                               const int32_t *mask, void *out, int batch, int seq,
+                               bbh_stream_t stream);
 bbh_status bbh_attention_block(bbh_workspace *ws, const bbh_model *m, int layer,
                                const void *hidden, const int32_t *mask, void *out,
                                int batch, int seq, bbh_stream_t stream);
@@ -221,6 +251,10 @@ bbh_status bbh_l2_normalize(void *x, int n, int batch, bbh_stream_t stream);
 /* Masked mean pool + L2 normalize fused (forward.cu:51-52), dim 384. */
 bbh_status bbh_pool_normalize(const void *hidden, const int32_t *mask, void *out,
                               int seq, int dim, int batch, bbh_stream_t stream);
+/* launch_gelu (src/kernels/gelu.h:9): x[i] = GELU(x[i]) in place, exact erf
+ * form, n >= 0 values.  On the hot path GELU runs inside the FFN1 GEMM
+ * epilogue; this entry point is the standalone operator. */
+bbh_status bbh_gelu(void *x, int n, bbh_stream_t stream);
 
 #ifdef __cplusplus
 }

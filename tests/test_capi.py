@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 34
+    assert len(names) == 39
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point
@@ -128,3 +128,23 @@ def test_product_path_fails_loudly_without_library(tmp_path, monkeypatch):
     monkeypatch.setattr(capi, "LIB_PATH", str(tmp_path / "libbbh.so"))
     with pytest.raises(RuntimeError, match="not built"):
         capi.lib()
+
+
+def test_weight_view_entry_points_validate_before_launch():
+    L = _lib()
+    from bbh import capi
+
+    aw, fw = capi.AttnWeights(), capi.FfnWeights()
+    assert L.bbh_model_layer(None, 0, ctypes.byref(aw), ctypes.byref(fw)) == 1
+    # range is checked before the handle is read
+    assert L.bbh_model_layer(ctypes.c_void_p(1), 6, None, None) == 1
+    assert b"out of range" in L.bbh_last_error()
+    fake = ctypes.c_void_p(256)
+    assert L.bbh_attention_block_w(None, fake, ctypes.byref(aw), fake, fake, 1, 16, None) == 1
+    assert L.bbh_ffn_block_w(None, fake, ctypes.byref(fw), fake, 1, 16, None) == 1
+    assert L.bbh_encoder_layer_w(None, fake, ctypes.byref(aw), ctypes.byref(fw), fake, fake, 1, 16,
+                                 None) == 1
+    # launch_gelu: n == 0 is a no-op, negative n and a null buffer are errors
+    assert L.bbh_gelu(None, 0, None) == 0
+    assert L.bbh_gelu(None, 5, None) == 1
+    assert L.bbh_gelu(fake, -1, None) == 1

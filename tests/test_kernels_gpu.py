@@ -28,6 +28,9 @@ GEMM_SHAPES = [
     (16, 1152, 384, False), (48, 384, 384, False), (1040, 1536, 384, True),
     (1024, 384, 1536, False), (3072, 1152, 384, False), (8192, 1536, 384, True),
     (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
+    # large-M tiles (cfg5 runs M = 131072 end to end)
+    (32768, 1152, 384, False), (32768, 1536, 384, True), (32768, 384, 384, False),
+    (32768, 384, 1536, False),
 ]
 
 
@@ -63,7 +66,8 @@ def test_linear_reference_kat(torch_cuda, kats, tag):
     assert np.abs(got - C).max() <= TOL
 
 
-@pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384)])
+@pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384),
+                                 (32768, 384), (32768, 1536)])
 def test_linear_residual_layernorm(torch_cuda, M, K):
     torch = torch_cuda
     from bbh import engine
@@ -243,6 +247,36 @@ def test_softmax_reference_kat(torch_cuda, kats):
     got = _np(x)
     assert cosine_rows(got.ravel(), kats["softmax_y"].ravel()) >= 0.9999
     assert np.abs(got - kats["softmax_y"]).max() <= 2e-3
+
+
+# ---- GELU ----------------------------------------------------------------------
+
+def test_gelu_reference_kat(torch_cuda, kats):
+    # tests/test_gelu.cu: exact GELU in place over 128 x 1536 fp16 values
+    torch = torch_cuda
+    from bbh import engine
+
+    x = to_dev(torch, kats["gelu_x"])
+    engine.launch_gelu(x, x.numel())
+    got, want = _np(x), kats["gelu_y"]
+    assert cosine_rows(got.ravel(), want.ravel()) >= 0.9999
+    assert np.abs(got - want).max() <= 4e-3  # half an fp16 ulp at |y| ~ 8
+
+
+def test_gelu_unaligned_and_ragged(torch_cuda, kats):
+    # a start 6 bytes past a 16-byte boundary and a length that is not a
+    # multiple of 8 take the one-value-per-thread kernel; nothing outside is touched
+    torch = torch_cuda
+    from bbh import engine
+
+    src = kats["gelu_x"][:1000]
+    x = to_dev(torch, src)
+    engine.launch_gelu(x[3:], 990)
+    got = _np(x)
+    want = O.gelu(src[3:993].astype(np.float32))
+    assert np.abs(got[3:993] - want).max() <= 4e-3
+    assert np.array_equal(got[:3], src[:3].astype(np.float32))
+    assert np.array_equal(got[993:], src[993:].astype(np.float32))
 
 
 # ---- pooling / normalize --------------------------------------------------------

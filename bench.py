@@ -4,8 +4,11 @@ Default workload: the synthetic varlen mix - 2000
 sentences, lognormal lengths clipped to [5, 64], consecutive batches of 64 in
 seeded order, each padded to round16(longest) (32 batches, eff 32/48/64).
 One step = one pass of bert_embed over all 32 pre-uploaded batches (the
-reference times passes over its corpus the same way, bench/corpus.cu:120-132).
-value = sentences/s over the K timed steps.
+reference times passes over its corpus the same way, bench/corpus.cu:120-132),
+through bbh_embed_batches: the batches are packed grouped by their padded
+length, so each run of equal-length batches executes as one forward (every
+batch keeps its own padding, so the executed work is unchanged), and the runs
+overlap on N_STREAMS streams.  value = sentences/s over the K timed steps.
 
 The same line also carries, as extra fields: configs[1] (batch 64 x seq 16)
 and configs[2] (batch 64 x seq 128) sent/s (300 timed iterations as
@@ -29,10 +32,13 @@ for _p in (ROOT, os.path.join(ROOT, "bert-by-hand_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-N_STREAMS = 8  # concurrent batches in the varlen pass (one workspace per stream; the
-#                runtime spreads streams over 4 hardware queues)
+N_STREAMS = 2  # concurrent forwards in the varlen pass (one workspace per stream)
+POOL_BATCH = 1024  # workspace rows per stream = POOL_BATCH * 64: the 21 batches of
+#                    padded length 48 (64,512 rows) run as one forward
 PEAK_FP16_DENSE = 2.5e15  # MI355X published dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
+EPI_OF_OP = {"qkv": "0 (bias)", "ffn1_gelu": "1 (bias+GELU)"}
+PROFILES = os.path.join(ROOT, "profiles")
 
 # Algorithmic FLOPs of one Linear: 2*M*N*K.
 LAYER_GEMMS = [  # (name, N, K, epilogue)
@@ -139,8 +145,8 @@ def main():
     # round-robin over a pool of N_STREAMS streams (one workspace each).
     batches = synth.varlen_mix()
     n_sent = sum(b[0].shape[0] for b in batches)
-    packed = engine.PackedBatches([b[:3] for b in batches])
-    pool = engine.Pool(N_STREAMS, 64, 64)
+    packed = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
+    pool = engine.Pool(N_STREAMS, POOL_BATCH, 64)
     emb_all = torch.empty((packed.rows, 384), dtype=torch.float16, device="cuda")
 
     def step():
@@ -183,9 +189,11 @@ def main():
         "data": "synthetic (seeded random-init MiniLM-L6 weights N(0,0.02), synthetic token ids)",
         "config": {"workload": "varlen mix: 2000 sentences, lognormal(median 12, sigma 0.5) "
                                "lengths clipped to [5,64], consecutive batches of 64 padded to "
-                               "round16(max); one step = bert_embed over all 32 batches, dealt "
-                               f"round-robin over {N_STREAMS} streams",
-                   "streams": N_STREAMS,
+                               "round16(max); one step = bert_embed over all 32 batches via "
+                               "bbh_embed_batches, batches packed grouped by padded length so "
+                               "each equal-length run is one forward (runs of 8/21/3 batches "
+                               f"at seq 32/48/64), runs on {N_STREAMS} streams",
+                   "streams": N_STREAMS, "pool_rows_per_stream": POOL_BATCH * 64,
                    "model": "MiniLM-L6 (6 layers, hidden 384, 12x32 heads, FFN 1536)",
                    "global_batch": 64, "seq_len": "32/48/64 (mean eff 45.8)",
                    "parallelism": "single GPU"},
@@ -195,28 +203,65 @@ def main():
     }
 
     # ---- dominant kernel of the default workload ---------------------------
-    buf = gemm_buffers(torch, 131072)
-    M_dom = 64 * 48  # the most common batch shape of the mix (21 of 32 batches)
-    per_kernel = {}
-    for name, N, K, epi in LAYER_GEMMS:
-        fn = gemm_runner(torch, engine, model, M_dom, N, K, epi, buf)
-        ms = timed(torch, fn, 200)
-        per_kernel[name] = {"ms": ms, "flops": 2.0 * M_dom * N * K}
-    qkv = torch.randn((M_dom, 1152), device="cuda").half()
-    msk = torch.ones((64, 48), dtype=torch.int32, device="cuda")
-    ctx = torch.empty((M_dom, 384), dtype=torch.float16, device="cuda")
-    ms_att = timed(torch, lambda: engine.launch_attention(qkv, msk, ctx, 64, 48), 200)
-    per_kernel["attention"] = {"ms": ms_att, "flops": 4.0 * 64 * 12 * 32 * 48 * 48}
-    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
-    d = per_kernel[dom]
-    ach = d["flops"] / (d["ms"] / 1e3)
-    out["roofline"] = {"bound": "mfma", "kernel": dom, "shape": f"M={M_dom} (batch 64 x eff 48)",
-                       "achieved": round(ach / 1e12, 2), "peak": PEAK_FP16_DENSE / 1e12,
-                       "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_DENSE, 4), "traffic": None,
-                       "avg_launch_us": round(d["ms"] * 1e3, 2)}
-    out["per_kernel_us_at_eff48"] = {k: round(v["ms"] * 1e3, 2) for k, v in per_kernel.items()}
-    log("per-kernel us at M=3072:", out["per_kernel_us_at_eff48"])
+    # The same passes again with the pool's per-launch timing on: a pair of
+    # HIP events on the pool stream around every op launch.  The dominant
+    # kernel is the (op, tile) class with the largest summed time per pass.
+    n_ops = 32 * 6 * 5
+    pool.timing(n_ops * args.steps)
+    for _ in range(args.steps):
+        step()
+    recs = pool.timing_read()
+    pool.timing(0)
+    classes = {}
+    for r in recs:
+        key = (r["op"], r["tile"], r["fused_ln"])
+        c = classes.setdefault(key, {"ms": 0.0, "n": 0, "flops": 0.0, "bytes": 0.0, "m": set()})
+        c["ms"] += r["ms"]
+        c["n"] += 1
+        c["m"].add(r["m"])
+        if r["op"] == "attention":
+            B, S, H = r["m"], r["n"], r["k"]
+            c["flops"] += 4.0 * B * H * 32 * S * S
+            c["bytes"] += B * S * (3 * 384 + 384) * 2.0
+        else:
+            M, N, K = r["m"], r["n"], r["k"]
+            c["flops"] += 2.0 * M * N * K
+            extra = M * N * 2.0 if r["op"] in ("o_proj_ln", "ffn2_ln") else 0.0  # residual
+            c["bytes"] += (M * K + N * K + M * N + N) * 2.0 + extra
+    per_op = {}
+    for (op, tile, fused), c in classes.items():
+        per_op[op] = per_op.get(op, 0.0) + c["ms"] / args.steps
+    key = max(classes, key=lambda k: classes[k]["ms"])
+    op, tile, fused = key
+    c = classes[key]
+    avg_s = c["ms"] / c["n"] / 1e3
+    ach = c["flops"] / c["n"] / avg_s
+    if op == "attention":
+        kname = "attention_kernel"
+    else:
+        epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else
+                                    "2 (bias+residual), then ln384_kernel")
+        kname = f"gemm_kernel<{engine.gemm_tile_name(tile)}, {epi}>"
+    traffic = None
+    tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
+    if os.path.exists(tfile):
+        t = json.load(open(tfile))
+        if t.get("kernel") == kname and t.get("m") == sorted(c["m"]):
+            traffic = t["traffic_bytes_per_launch"]
+    out["roofline"] = {
+        "bound": "mfma", "achieved": round(ach / 1e12, 2), "peak": PEAK_FP16_DENSE / 1e12,
+        "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_DENSE, 4), "traffic": traffic,
+        "kernel": kname, "op": op, "m": sorted(c["m"]),
+        "launches_per_step": c["n"] // args.steps,
+        "avg_launch_us": round(avg_s * 1e6, 2),
+        "algorithmic_flops_per_launch": round(c["flops"] / c["n"]),
+        "algorithmic_bytes_per_launch": round(c["bytes"] / c["n"]),
+        "share_of_op_time": round(c["ms"] / sum(v["ms"] for v in classes.values()), 3)}
+    out["op_ms_per_step"] = {k: round(v, 4) for k, v in sorted(per_op.items())}
+    log("roofline", out["roofline"])
+    log("op ms per step", out["op_ms_per_step"])
 
+    buf = gemm_buffers(torch, 131072)
     if not args.no_extras:
         # ---- batch 64 x seq 16 / 128 ----------------
         for tag, seq in (("cfg2_b64_s16", 16), ("cfg3_b64_s128", 128)):

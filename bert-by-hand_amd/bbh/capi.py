@@ -27,6 +27,12 @@ class FfnWeights(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in ("inter_w", "inter_b", "out_w", "out_b", "ln_w", "ln_b")]
 
 
+class LaunchTime(ctypes.Structure):
+    """bbh_launch_time: one timed op launch of a pool."""
+    _fields_ = [("op", c_int), ("tile", c_int), ("fused_ln", c_int), ("m", c_int), ("n", c_int),
+                ("k", c_int), ("ms", c_float)]
+
+
 _AWp, _FWp = ctypes.POINTER(AttnWeights), ctypes.POINTER(FfnWeights)
 
 # name -> (restype, argtypes); every symbol declared in include/bbh.h.
@@ -53,6 +59,10 @@ SIGNATURES = {
     "bbh_pool_free": (c_int, [c_void_p]),
     "bbh_embed_batches": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "bbh_pool_timing": (c_int, [c_void_p, c_int]),
+    "bbh_pool_timing_read": (c_int, [c_void_p, ctypes.POINTER(LaunchTime), c_int,
+                                     ctypes.POINTER(c_int)]),
+    "bbh_gemm_tile_name": (c_char_p, [c_int]),
     "bbh_model_layer": (c_int, [c_void_p, c_int, _AWp, _FWp]),
     "bbh_attention_block_w": (c_int, [c_void_p, c_void_p, _AWp, c_void_p, c_void_p, c_int, c_int,
                                       c_void_p]),

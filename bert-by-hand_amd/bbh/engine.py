@@ -131,6 +131,21 @@ class Pool:
         self.handle = ctypes.c_void_p()
         call("bbh_pool_create", n_streams, max_batch, max_seq, ctypes.byref(self.handle))
 
+    def timing(self, capacity: int):
+        """Start timing each op of later embed_batches calls (0 stops)."""
+        call("bbh_pool_timing", self.handle, capacity)
+
+    OPS = {1: "qkv", 2: "attention", 3: "o_proj_ln", 4: "ffn1_gelu", 5: "ffn2_ln"}
+
+    def timing_read(self):
+        """The recorded launches: dicts of op, tile, fused_ln, m, n, k, ms."""
+        cnt = ctypes.c_int()
+        call("bbh_pool_timing_read", self.handle, None, 0, ctypes.byref(cnt))
+        buf = (capi.LaunchTime * max(cnt.value, 1))()
+        call("bbh_pool_timing_read", self.handle, buf, cnt.value, ctypes.byref(cnt))
+        return [dict(op=self.OPS[r.op], tile=r.tile, fused_ln=bool(r.fused_ln), m=r.m, n=r.n,
+                     k=r.k, ms=r.ms) for r in buf[:cnt.value]]
+
     def close(self):
         if self.handle:
             call("bbh_pool_free", self.handle)
@@ -145,10 +160,21 @@ class Pool:
 
 class PackedBatches:
     """Batches packed back to back in device memory for embed_batches:
-    batch i = (ids, types, mask) of shape (B_i, S_i)."""
+    batch i = (ids, types, mask) of shape (B_i, S_i).
 
-    def __init__(self, batches):
+    With group_by_seq=True the batches are stable-sorted by S_i before
+    packing, so equal-length batches are adjacent and embed_batches runs each
+    such run as one larger forward; every batch keeps its own padding.
+    `order` is the packed position -> input batch index map, and
+    `unpermute(emb)` returns the embeddings in input sentence order."""
+
+    def __init__(self, batches, group_by_seq: bool = False):
         torch = _torch()
+        n = len(batches)
+        seqs_in = [int(b[0].shape[1]) for b in batches]
+        order = sorted(range(n), key=lambda i: seqs_in[i]) if group_by_seq else list(range(n))
+        self.order = np.asarray(order, np.int64)
+        batches = [batches[i] for i in order]
         sizes = [int(b[0].shape[0]) for b in batches]
         seqs = [int(b[0].shape[1]) for b in batches]
         toks = [b * s for b, s in zip(sizes, seqs)]
@@ -159,7 +185,21 @@ class PackedBatches:
         self.rows = int(sum(sizes))
         cat = lambda k: torch.from_numpy(np.concatenate([np.asarray(b[k]).reshape(-1) for b in batches]).astype(np.int32)).cuda()  # noqa: E731
         self.ids, self.types, self.mask = cat(0), cat(1), cat(2)
-        self.n = len(batches)
+        self.n = n
+        # packed sentence row -> input sentence row
+        in_sizes = np.zeros(n, np.int64)
+        in_sizes[self.order] = self.sizes
+        in_start = np.concatenate([[0], np.cumsum(in_sizes)[:-1]])
+        self._rows_src = np.concatenate(
+            [in_start[i] + np.arange(in_sizes[i]) for i in self.order]).astype(np.int64) \
+            if n else np.zeros(0, np.int64)
+
+    def unpermute(self, emb):
+        """Embeddings (rows, 384) in packed order -> input sentence order."""
+        torch = _torch()
+        out = torch.empty_like(emb)
+        out[torch.from_numpy(self._rows_src).to(emb.device)] = emb
+        return out
 
 
 def embed_batches(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=None):
@@ -316,6 +356,11 @@ def launch_pool_normalize(hidden, mask, out, seq, batch=1, stream=None):
     call("bbh_pool_normalize", _ptr(hidden), _ptr(mask), _ptr(out), seq, HIDDEN, batch,
          _stream(stream))
     return out
+
+
+def gemm_tile_name(tile: int) -> str:
+    """Template argument of the GEMM kernel symbol for a tile id."""
+    return capi.lib().bbh_gemm_tile_name(tile).decode()
 
 
 BBHError = capi.BBHError

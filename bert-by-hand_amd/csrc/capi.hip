@@ -232,33 +232,67 @@ bbh_status misaligned(const char* what) {
 
 const float kScale = 0.17677669529663687f;  // 1 / sqrt(32), src/model/encoder.cu:28
 
+// Pairs of timing events around op launches (bbh_pool_timing).
+struct OpTimer {
+  std::vector<hipEvent_t> ev;  // two per slot
+  std::vector<bbh_launch_time> rec;
+  int used = 0;
+  ~OpTimer() {
+    for (auto e : ev) (void)hipEventDestroy(e);
+  }
+};
+
+// launch() between a pair of events on s when t has a free slot.
+template <class F>
+bbh_status timed_op(OpTimer* t, hipStream_t s, const bbh_launch_time& meta, F&& launch) {
+  int slot = -1;
+  if (t && t->used < (int)t->rec.size() && hipEventRecord(t->ev[2 * t->used], s) == hipSuccess)
+    slot = t->used++;
+  const bbh_status st = launch();
+  if (slot >= 0) {
+    t->rec[slot] = meta;
+    (void)hipEventRecord(t->ev[2 * slot + 1], s);
+  }
+  return st;
+}
+
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                               const int32_t* mask, f16* out, int batch, int seq,
-                               hipStream_t s) {
-  const int M = batch * seq;
-  BBH_TRY(check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * BBH_HIDDEN,
-                                 BBH_HIDDEN, bbh::Act::kNone, s),
-                       "qkv gemm"));
-  BBH_TRY(check_launch(bbh::attention(ws->qkv, mask, ws->ctx, batch, BBH_NUM_HEADS, seq,
-                                      kScale, s),
-                       "attention"));
-  BBH_TRY(check_launch(bbh::gemm_residual_ln(ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g, L.ln1_b,
-                                             out, M, BBH_HIDDEN, BBH_LAYER_NORM_EPS, s),
-                       "o-proj gemm+ln"));
-  return BBH_OK;
+                               const int32_t* mask, f16* out, int batch, int seq, hipStream_t s,
+                               OpTimer* t = nullptr) {
+  const int M = batch * seq, H = BBH_HIDDEN;
+  BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H), 0, M, 3 * H, H, 0.f}, [&] {
+    return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
+                                  bbh::Act::kNone, s),
+                        "qkv gemm");
+  }));
+  BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, batch, seq, BBH_NUM_HEADS, 0.f}, [&] {
+    return check_launch(bbh::attention(ws->qkv, mask, ws->ctx, batch, BBH_NUM_HEADS, seq,
+                                       kScale, s),
+                        "attention");
+  }));
+  bool fused;
+  const int tile = bbh::gemm_residual_ln_tile(M, H, &fused);
+  return timed_op(t, s, {BBH_OP_O_PROJ_LN, tile, fused ? 1 : 0, M, H, H, 0.f}, [&] {
+    return check_launch(bbh::gemm_residual_ln(ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g, L.ln1_b,
+                                              out, M, H, BBH_LAYER_NORM_EPS, s),
+                        "o-proj gemm+ln");
+  });
 }
 
 bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                         f16* out, int batch, int seq, hipStream_t s) {
-  const int M = batch * seq;
-  BBH_TRY(check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, BBH_FFN_DIM, BBH_HIDDEN,
-                                 bbh::Act::kGelu, s),
-                       "ffn1 gemm"));
-  BBH_TRY(check_launch(bbh::gemm_residual_ln(ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
-                                             L.ln2_b, out, M, BBH_FFN_DIM, BBH_LAYER_NORM_EPS,
-                                             s),
-                       "ffn2 gemm+ln"));
-  return BBH_OK;
+                         f16* out, int batch, int seq, hipStream_t s, OpTimer* t = nullptr) {
+  const int M = batch * seq, H = BBH_HIDDEN, F = BBH_FFN_DIM;
+  BBH_TRY(timed_op(t, s, {BBH_OP_FFN1_GELU, bbh::gemm_tile(M, F, H), 0, M, F, H, 0.f}, [&] {
+    return check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, F, H, bbh::Act::kGelu, s),
+                        "ffn1 gemm");
+  }));
+  bool fused;
+  const int tile = bbh::gemm_residual_ln_tile(M, F, &fused);
+  return timed_op(t, s, {BBH_OP_FFN2_LN, tile, fused ? 1 : 0, M, H, F, 0.f}, [&] {
+    return check_launch(bbh::gemm_residual_ln(ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
+                                              L.ln2_b, out, M, F, BBH_LAYER_NORM_EPS, s),
+                        "ffn2 gemm+ln");
+  });
 }
 
 // Embeddings + 6 layers; the last layer writes `final_out` (which may be
@@ -266,15 +300,15 @@ bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16
 // same thread overwrites it).
 bbh_status run_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
                       const int32_t* types, const int32_t* mask, f16* final_out, int batch,
-                      int seq, hipStream_t s) {
+                      int seq, hipStream_t s, OpTimer* t = nullptr) {
   BBH_TRY(check_launch(bbh::embedding_ln(ids, types, m->word, m->pos, m->type, m->emb_g,
                                          m->emb_b, ws->ping, batch, seq, BBH_LAYER_NORM_EPS, s),
                        "embedding+ln"));
   f16* cur = ws->ping;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
-    BBH_TRY(run_attention_block(ws, m->layers[i], cur, mask, ws->attn_out, batch, seq, s));
-    BBH_TRY(run_ffn_block(ws, m->layers[i], ws->attn_out, nxt, batch, seq, s));
+    BBH_TRY(run_attention_block(ws, m->layers[i], cur, mask, ws->attn_out, batch, seq, s, t));
+    BBH_TRY(run_ffn_block(ws, m->layers[i], ws->attn_out, nxt, batch, seq, s, t));
     cur = nxt;
   }
   return BBH_OK;
@@ -444,9 +478,12 @@ struct bbh_pool {
   std::vector<hipEvent_t> done;  // one per stream, recorded at the end of a call
   hipEvent_t fork = nullptr;
   std::vector<bbh_workspace*> ws;
+  OpTimer* timer = nullptr;  // bbh_pool_timing
 };
 
 static void pool_release(bbh_pool* p) {
+  for (auto st : p->streams) (void)hipStreamSynchronize(st);
+  delete p->timer;
   for (auto w : p->ws) bbh_workspace_free(w);
   for (auto e : p->done) (void)hipEventDestroy(e);
   for (auto s : p->streams) (void)hipStreamDestroy(s);
@@ -516,19 +553,43 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
       return fail(BBH_ERR_INVALID_ARG, "batch " + std::to_string(i) + ": negative offset");
   }
   if (n_batches == 0) return BBH_OK;
+  // Runs of consecutive batches with one seq that sit back to back in the
+  // token arrays and in emb are one (sum of batches, seq) forward, up to a
+  // workspace's rows: sentences are independent, so each keeps exactly the
+  // embedding it gets alone, while the kernels see a larger M.
+  struct Run {
+    int first, batch;
+  };
+  std::vector<Run> runs;
+  const size_t cap = pool->ws[0]->rows;
+  for (int i = 0; i < n_batches; ++i) {
+    if (i > 0 && !runs.empty()) {
+      Run& r = runs.back();
+      const int k = i - 1;
+      if (seqs[i] == seqs[k] &&
+          tok_offsets[i] == tok_offsets[k] + (int64_t)batch_sizes[k] * seqs[k] &&
+          emb_rows[i] == emb_rows[k] + batch_sizes[k] &&
+          (size_t)(r.batch + batch_sizes[i]) * seqs[i] <= cap) {
+        r.batch += batch_sizes[i];
+        continue;
+      }
+    }
+    runs.push_back({i, batch_sizes[i]});
+  }
+  const int n_runs = (int)runs.size();
   const hipStream_t caller = S(stream);
   BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
-  const int used = n_batches < n ? n_batches : n;
+  const int used = n_runs < n ? n_runs : n;
   for (int j = 0; j < used; ++j)
     BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
-  for (int i = 0; i < n_batches; ++i) {
-    const int j = i % n;
+  for (int r = 0; r < n_runs; ++r) {
+    const int j = r % n, i = runs[r].first, batch = runs[r].batch, seq = seqs[i];
     const int64_t o = tok_offsets[i];
     f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
     bbh_workspace* w = pool->ws[j];
-    BBH_TRY(run_encode(w, m, ids + o, types + o, mask + o, w->attn_out, batch_sizes[i], seqs[i],
-                       pool->streams[j]));
-    BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out, mask + o, out, batch_sizes[i], seqs[i],
+    BBH_TRY(run_encode(w, m, ids + o, types + o, mask + o, w->attn_out, batch, seq,
+                       pool->streams[j], pool->timer));
+    BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out, mask + o, out, batch, seq,
                                              pool->streams[j]),
                          "pool+normalize"));
   }
@@ -538,6 +599,45 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
   }
   return BBH_OK;
 }
+
+bbh_status bbh_pool_timing(bbh_pool* pool, int capacity) {
+  if (!pool) return fail(BBH_ERR_INVALID_ARG, "null pool");
+  if (capacity < 0 || capacity > (1 << 16))
+    return fail(BBH_ERR_INVALID_ARG, "timing capacity must be in [0, 65536]");
+  for (auto st : pool->streams) BBH_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  delete pool->timer;
+  pool->timer = nullptr;
+  if (capacity == 0) return BBH_OK;
+  auto* t = new OpTimer;
+  t->ev.assign(2 * (size_t)capacity, nullptr);
+  for (auto& e : t->ev) {
+    const hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      e = nullptr;
+      delete t;
+      return fail(BBH_ERR_HIP, std::string("hipEventCreate: ") + hipGetErrorName(err));
+    }
+  }
+  t->rec.assign(capacity, bbh_launch_time{});
+  pool->timer = t;
+  return BBH_OK;
+}
+
+bbh_status bbh_pool_timing_read(bbh_pool* pool, bbh_launch_time* out, int max, int* count) {
+  if (!pool || !count || (max > 0 && !out)) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  *count = 0;
+  if (!pool->timer) return BBH_OK;
+  for (auto st : pool->streams) BBH_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  OpTimer* t = pool->timer;
+  for (int i = 0; i < t->used; ++i)
+    BBH_HIP(hipEventElapsedTime(&t->rec[i].ms, t->ev[2 * i], t->ev[2 * i + 1]),
+            "hipEventElapsedTime");
+  for (int i = 0; i < t->used && i < max; ++i) out[i] = t->rec[i];
+  *count = t->used;
+  return BBH_OK;
+}
+
+const char* bbh_gemm_tile_name(int tile) { return bbh::gemm_tile_name(tile); }
 
 static bbh_status check_layer(const bbh_workspace* ws, const bbh_model* m, int layer,
                               const void* hidden, const void* out, int batch, int seq) {

@@ -508,55 +508,62 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 //   27  128x192   64x96      PD 3   80 KB
 //   28  128x384   64x96 (8w) PD 2  128 KB   (owns whole rows)
 //   29  256x128   128x64     PD 3   96 KB
+// Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD>, epilogue>.
+// The table itself: X(id, BM, BN, WM, WN, SA, PD), ids dense from 0.
+#define BBH_TILES(X)          \
+  X(0, 64, 64, 2, 2, 4, 0)    \
+  X(1, 64, 128, 2, 2, 4, 0)   \
+  X(2, 128, 64, 2, 2, 4, 0)   \
+  X(3, 128, 128, 2, 2, 4, 0)  \
+  X(4, 256, 128, 2, 2, 3, 0)  \
+  X(5, 128, 384, 1, 4, 4, 0)  \
+  X(6, 64, 384, 1, 4, 4, 0)   \
+  X(7, 32, 128, 1, 4, 4, 0)   \
+  X(8, 128, 192, 2, 2, 4, 0)  \
+  X(9, 256, 192, 2, 2, 3, 0)  \
+  X(10, 32, 384, 1, 4, 4, 0)  \
+  X(11, 128, 384, 1, 4, 3, 0) \
+  X(12, 256, 192, 2, 2, 2, 0) \
+  X(13, 128, 192, 2, 2, 3, 0) \
+  X(14, 64, 384, 1, 4, 2, 0)  \
+  X(15, 128, 128, 2, 2, 2, 0) \
+  X(16, 64, 128, 2, 2, 6, 0)  \
+  X(17, 256, 384, 2, 4, 2, 0) \
+  X(18, 128, 384, 2, 4, 4, 0) \
+  X(19, 256, 192, 4, 2, 3, 0) \
+  X(20, 256, 128, 4, 2, 3, 0) \
+  X(21, 128, 256, 2, 4, 4, 0) \
+  X(22, 128, 128, 2, 2, 2, 3) \
+  X(23, 128, 128, 2, 2, 2, 4) \
+  X(24, 128, 256, 2, 4, 2, 2) \
+  X(25, 256, 128, 4, 2, 2, 2) \
+  X(26, 64, 64, 2, 2, 2, 4)   \
+  X(27, 128, 192, 2, 2, 2, 3) \
+  X(28, 128, 384, 2, 4, 2, 2) \
+  X(29, 256, 128, 2, 2, 2, 3)
+
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
                      const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
                      hipStream_t s) {
-#define BBH_CFG(ID, BM, BN, WM, WN, SA, ...)                                                        \
-  case ID:                                                                                    \
-    return launch<Cfg<BM, BN, WM, WN, SA, ##__VA_ARGS__>, EPI>(A, W, bias, residual, gamma, beta, out, M, N, \
-                                                K, eps, s);
-  switch (id) {
-    BBH_CFG(0, 64, 64, 2, 2, 4)
-    BBH_CFG(1, 64, 128, 2, 2, 4)
-    BBH_CFG(2, 128, 64, 2, 2, 4)
-    BBH_CFG(3, 128, 128, 2, 2, 4)
-    BBH_CFG(4, 256, 128, 2, 2, 3)
-    BBH_CFG(5, 128, 384, 1, 4, 4)
-    BBH_CFG(6, 64, 384, 1, 4, 4)
-    BBH_CFG(7, 32, 128, 1, 4, 4)
-    BBH_CFG(8, 128, 192, 2, 2, 4)
-    BBH_CFG(9, 256, 192, 2, 2, 3)
-    BBH_CFG(10, 32, 384, 1, 4, 4)
-    BBH_CFG(11, 128, 384, 1, 4, 3)
-    BBH_CFG(12, 256, 192, 2, 2, 2)
-    BBH_CFG(13, 128, 192, 2, 2, 3)
-    BBH_CFG(14, 64, 384, 1, 4, 2)
-    BBH_CFG(15, 128, 128, 2, 2, 2)
-    BBH_CFG(16, 64, 128, 2, 2, 6)
-    BBH_CFG(17, 256, 384, 2, 4, 2)
-    BBH_CFG(18, 128, 384, 2, 4, 4)
-    BBH_CFG(19, 256, 192, 4, 2, 3)
-    BBH_CFG(20, 256, 128, 4, 2, 3)
-    BBH_CFG(21, 128, 256, 2, 4, 4)
-    BBH_CFG(22, 128, 128, 2, 2, 2, 3)
-    BBH_CFG(23, 128, 128, 2, 2, 2, 4)
-    BBH_CFG(24, 128, 256, 2, 4, 2, 2)
-    BBH_CFG(25, 256, 128, 4, 2, 2, 2)
-    BBH_CFG(26, 64, 64, 2, 2, 2, 4)
-    BBH_CFG(27, 128, 192, 2, 2, 2, 3)
-    BBH_CFG(28, 128, 384, 2, 4, 2, 2)
-    BBH_CFG(29, 256, 128, 2, 2, 2, 3)
-  }
-#undef BBH_CFG
+#define BBH_CASE(ID, BM, BN, WM, WN, SA, PD)                                                 \
+  case ID:                                                                                 \
+    return launch<Cfg<BM, BN, WM, WN, SA, PD>, EPI>(A, W, bias, residual, gamma, beta, out, \
+                                                    M, N, K, eps, s);
+  switch (id) { BBH_TILES(BBH_CASE) }
+#undef BBH_CASE
   return hipErrorInvalidValue;
 }
 
-// Tile choice per shape, from sweeps of every id at the path's shapes on
-// MI355X (M = 2048..8192 for the varlen batches, 131072 for batch 256 x 512).
-constexpr int kBnOf[] = {64,  128, 64,  128, 128, 384, 384, 128, 192, 192, 384,
-                         384, 192, 192, 384, 128, 128, 384, 384, 192, 128, 256,
-                         128, 128, 256, 128, 64,  192, 384, 128};
+#define BBH_BN(ID, BM, BN, WM, WN, SA, PD) BN,
+constexpr int kBnOf[] = {BBH_TILES(BBH_BN)};
+#undef BBH_BN
+constexpr int kTiles = sizeof(kBnOf) / sizeof(kBnOf[0]);
+
+#define BBH_NAME(ID, BM, BN, WM, WN, SA, PD) \
+  "Cfg<" #BM "," #BN "," #WM "," #WN "," #SA "," #PD ">",
+const char* const kTileName[] = {BBH_TILES(BBH_NAME)};
+#undef BBH_NAME
 
 // Tile config per shape, from sweeps on MI355X over the encoder's four
 // shapes (N, K) = (1152, 384) QKV, (1536, 384) FFN1, (384, 384) O-proj and
@@ -582,6 +589,21 @@ int pick_plain(int M, int N, int K) {
 
 bool gemm_mfma_ok(int N, int K) { return N % 64 == 0 && K % 64 == 0; }
 
+int gemm_tile(int M, int N, int K) { return gemm_mfma_ok(N, K) ? pick_plain(M, N, K) : -1; }
+
+// Large M: one kernel whose 128x384 tile owns whole rows.  Smaller M: a tile
+// that owns whole rows leaves most CUs idle and streams all of W per
+// workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
+// (in place over y) and the row LayerNorm follows as its own pass.
+int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
+  *fused_ln = M > 24576;
+  return *fused_ln ? 18 : pick_plain(M, kHidden, K);
+}
+
+const char* gemm_tile_name(int tile) {
+  return (tile >= 0 && tile < kTiles) ? kTileName[tile] : "generic";
+}
+
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N, int K,
                 Act act, hipStream_t s) {
   const bool gelu = act == Act::kGelu;
@@ -601,14 +623,12 @@ hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int 
 hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f16* residual,
                             const f16* gamma, const f16* beta, f16* y, int M, int K, float eps,
                             hipStream_t s) {
-  // Large M: one kernel whose 128x384 tile owns whole rows.  Smaller M: a
-  // tile that owns whole rows leaves most CUs idle and streams all of W per
-  // workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
-  // (in place over y) and the row LayerNorm follows as its own pass.
-  if (M > 24576)
-    return launch_id<kLayerNorm>(18, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
-  hipError_t e = launch_id<kResidual>(pick_plain(M, kHidden, K), A, W, bias, residual, nullptr,
-                                      nullptr, y, M, kHidden, K, eps, s);
+  bool fused;
+  const int id = gemm_residual_ln_tile(M, K, &fused);
+  if (fused)
+    return launch_id<kLayerNorm>(id, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
+  hipError_t e = launch_id<kResidual>(id, A, W, bias, residual, nullptr, nullptr, y, M, kHidden, K,
+                                      eps, s);
   if (e != hipSuccess) return e;
   return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);
 }

@@ -17,6 +17,13 @@ bool gemm_mfma_ok(int N, int K);
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N,
                 int K, Act act, hipStream_t s);
 
+// Tile configuration gemm() / gemm_residual_ln() launch for a shape (-1: the
+// plain tiled kernel), whether the LayerNorm is inside the GEMM kernel, and
+// the configuration's name as it appears in the kernel symbol.
+int gemm_tile(int M, int N, int K);
+int gemm_residual_ln_tile(int M, int K, bool* fused_ln);
+const char* gemm_tile_name(int tile);
+
 // y(M,384) = LN(A(M,K) . W(384,K)^T + bias + residual) * gamma + beta.
 // y may alias residual.  K % 64 == 0.
 hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,

@@ -127,10 +127,16 @@ bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
  * sequential corpus loop (bench/corpus.cu:64-77,120-132).  Batch i reads its
  * (batch_sizes[i], seqs[i]) ids/types/mask starting at element
  * tok_offsets[i] of the device arrays and writes batch_sizes[i] rows of emb
- * starting at row emb_rows[i].  The size/offset arrays are HOST arrays.  The
- * call orders itself after prior work on `stream` and makes later work on
- * `stream` wait for all batches; it returns without a host sync.  A pool must
- * not be used by two overlapping calls. */
+ * starting at row emb_rows[i].  The size/offset arrays are HOST arrays.
+ * Consecutive batches with the same seq that are adjacent both in the token
+ * arrays and in emb run as one forward of their summed batch, up to a pool
+ * workspace's max_batch*max_seq rows, so a caller that packs equal-seq
+ * batches together gets larger kernels with every batch's padding unchanged
+ * (the reference's corpus benchmark instead re-sorts sentences by length,
+ * bench/corpus.cu:79-118).  Every sentence still gets the embedding it gets
+ * alone, since sentences never interact.  The call orders itself after prior work on
+ * `stream` and makes later work on `stream` wait for all batches; it returns
+ * without a host sync.  A pool must not be used by two overlapping calls. */
 typedef struct bbh_pool bbh_pool;
 bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
 bbh_status bbh_pool_free(bbh_pool *pool);
@@ -139,6 +145,35 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
                              const int64_t *tok_offsets, const int *batch_sizes,
                              const int *seqs, const int64_t *emb_rows, void *emb,
                              int n_batches, bbh_stream_t stream);
+
+/* ---- per-launch timing of a pool ---------------------------------------------
+ * HIP-event timing of each encoder op that bbh_embed_batches launches (the
+ * reference times whole forwards with CUDA events, src/core/timer.h:36-39).
+ * bbh_pool_timing(pool, capacity) starts a new record: a pair of events goes
+ * on the launching pool stream around every op of every forward, for the
+ * first `capacity` ops (later ones run untimed).  capacity 0 stops timing and
+ * releases the events.  bbh_pool_timing_read waits for the pool streams, then
+ * copies up to `max` records in launch order and sets *count to the number
+ * recorded. */
+typedef enum bbh_op {
+  BBH_OP_QKV = 1,       /* fused QKV Linear */
+  BBH_OP_ATTENTION = 2, /* masked multi-head attention */
+  BBH_OP_O_PROJ_LN = 3, /* attention output Linear + residual LayerNorm */
+  BBH_OP_FFN1_GELU = 4, /* intermediate Linear + GELU */
+  BBH_OP_FFN2_LN = 5    /* output Linear + residual LayerNorm */
+} bbh_op;
+typedef struct bbh_launch_time {
+  int op;       /* bbh_op */
+  int tile;     /* GEMM tile configuration (bbh_gemm_tile_name); -1 for attention */
+  int fused_ln; /* LayerNorm ops: 1 inside the GEMM kernel, 0 a second kernel timed with it */
+  int m, n, k;  /* GEMM (M, N, K); attention (batch, seq, heads) */
+  float ms;     /* time between the pair of events */
+} bbh_launch_time;
+bbh_status bbh_pool_timing(bbh_pool *pool, int capacity);
+bbh_status bbh_pool_timing_read(bbh_pool *pool, bbh_launch_time *out, int max, int *count);
+/* "Cfg<BM,BN,WM,WN,SA,PD>" of a GEMM tile configuration, the template
+ * argument in the kernel symbol gemm_kernel<Cfg<...>, epilogue>. */
+const char *bbh_gemm_tile_name(int tile);
 
 /* ---- weight views (src/model/encoder.h:11-22,37-40) -------------------------
  * Device pointers of one encoder layer's fp16 tensors, the reference's

@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 39
+    assert len(names) == 42
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point
@@ -148,3 +148,13 @@ def test_weight_view_entry_points_validate_before_launch():
     assert L.bbh_gelu(None, 0, None) == 0
     assert L.bbh_gelu(None, 5, None) == 1
     assert L.bbh_gelu(fake, -1, None) == 1
+
+
+def test_tile_names_and_timing_arguments():
+    L = _lib()
+    assert L.bbh_gemm_tile_name(23) == b"Cfg<128,128,2,2,2,4>"
+    assert L.bbh_gemm_tile_name(0) == b"Cfg<64,64,2,2,4,0>"
+    assert L.bbh_gemm_tile_name(-1) == b"generic" and L.bbh_gemm_tile_name(999) == b"generic"
+    cnt = ctypes.c_int(7)
+    assert L.bbh_pool_timing(None, 16) == 1
+    assert L.bbh_pool_timing_read(None, None, 0, ctypes.byref(cnt)) == 1

@@ -219,3 +219,25 @@ def test_pool_embed_batches_equals_sequential(torch_cuda, ws, model):
         engine.embed_batches(small, model, packed)
     small.close()
     pool.close()
+
+
+@pytest.mark.parametrize("max_batch", [256, 1024])
+def test_pool_merges_equal_seq_batches(torch_cuda, ws, model, max_batch):
+    # Length-grouped packing: each run of equal-seq batches executes as one
+    # forward of up to max_batch*64 rows (16384, or 65536 where the O-proj and
+    # FFN2 LayerNorms fuse into the GEMM).  Every sentence matches its own
+    # batch's forward up to fp32 reduction-order noise.
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    batches = synth.varlen_mix()
+    packed = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
+    assert list(packed.seqs) == sorted(packed.seqs)
+    pool = engine.Pool(3, max_batch, 64)
+    got = _np(packed.unpermute(engine.embed_batches(pool, model, packed)))
+    torch.cuda.synchronize()
+    pool.close()
+    want = np.concatenate([_embed(torch, ws, model, *b[:3]) for b in batches])
+    assert got.shape == want.shape == (2000, 384)
+    assert np.abs(got - want).max() <= 2e-3
+    assert cosine_rows(got, want).min() >= 0.99999

@@ -122,6 +122,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="only the varlen workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only time a device-to-device copy of BYTES (the calibration kernel "
+                         "for the HBM byte counters, and the practical copy bandwidth)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -136,6 +139,15 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        n = args.copy_probe // 2
+        src = torch.ones(n, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        ms = timed(torch, lambda: dst.copy_(src), 5, warmup=2)
+        print(json.dumps({"copy_bytes": 2 * n, "ms": round(ms, 4),
+                          "read_plus_write_GB_per_s": round(4 * n / (ms / 1e3) / 1e9, 1)}),
+              flush=True)
+        return
     weights = synth.make_weights(0)
     model = engine.Model.from_weights(weights)
     ws = engine.Workspace(256, 512)

@@ -415,6 +415,9 @@ bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out)
     return fail(BBH_ERR_SEQ_ALIGN, "max_seq must be a multiple of 16");
   if (max_seq > BBH_MAX_POSITION)
     return fail(BBH_ERR_CAPACITY, "max_seq exceeds max position 512");
+  if ((size_t)max_batch * max_seq > BBH_MAX_ROWS)
+    return fail(BBH_ERR_CAPACITY, "max_batch*max_seq exceeds " + std::to_string(BBH_MAX_ROWS) +
+                                      " rows");
   bbh_workspace* ws = new bbh_workspace();
   ws->max_batch = max_batch;
   ws->max_seq = max_seq;

@@ -45,6 +45,9 @@ extern "C" {
 #define BBH_LAYER_NORM_EPS 1e-12f
 #define BBH_SEQ_ALIGN 16   /* seq must be a multiple of this (bench/bench.cu:63) */
 #define BBH_NUM_PARAMS 101 /* state_dict tensors without the pooler */
+/* Most token rows (batch*seq) a workspace holds: 2048 x 512, which keeps
+ * every rows x 1536 element count of the activations below 2^31. */
+#define BBH_MAX_ROWS (1 << 20)
 
 typedef enum bbh_status {
   BBH_OK = 0,
@@ -93,8 +96,9 @@ size_t bbh_model_device_bytes(const bbh_model *m);
  * Replaces make_workspace(batch) (src/model/workspace.h:20-36).  The
  * reference sizes every buffer for SEQ_LEN = 128 tokens per row; here
  * max_seq is a runtime capacity (multiple of 16, at most 512) so batch 256 x
- * seq 512 fits.  All scratch for any bbh_embed / bbh_encode with
- * batch <= max_batch and seq <= max_seq is allocated here, once. */
+ * seq 512 fits; max_batch*max_seq <= BBH_MAX_ROWS.  All scratch for any
+ * bbh_embed / bbh_encode with batch*seq <= max_batch*max_seq and
+ * seq <= max_seq is allocated here, once. */
 bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace **out);
 bbh_status bbh_workspace_free(bbh_workspace *ws);
 size_t bbh_workspace_bytes(int max_batch, int max_seq);
@@ -134,9 +138,10 @@ bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
  * batches together gets larger kernels with every batch's padding unchanged
  * (the reference's corpus benchmark instead re-sorts sentences by length,
  * bench/corpus.cu:79-118).  Every sentence still gets the embedding it gets
- * alone, since sentences never interact.  The call orders itself after prior work on
- * `stream` and makes later work on `stream` wait for all batches; it returns
- * without a host sync.  A pool must not be used by two overlapping calls. */
+ * alone, since sentences never interact.  The call orders itself after prior
+ * work on `stream` and makes later work on `stream` wait for all batches; it
+ * returns without a host sync.  A pool must not be used by two overlapping
+ * calls. */
 typedef struct bbh_pool bbh_pool;
 bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
 bbh_status bbh_pool_free(bbh_pool *pool);

@@ -82,6 +82,7 @@ def test_null_arguments_rejected_without_device_work():
     assert L.bbh_workspace_create(0, 16, ctypes.byref(h)) == 1
     assert L.bbh_workspace_create(4, 24, ctypes.byref(h)) == 2  # seq % 16
     assert L.bbh_workspace_create(4, 528, ctypes.byref(h)) == 3  # > 512
+    assert L.bbh_workspace_create(2049, 512, ctypes.byref(h)) == 3  # > 2^20 rows
     with pytest.raises(capi.BBHError) as e:
         capi.call("bbh_model_from_host", None, 101, ctypes.byref(h))
     assert e.value.name == "BBH_ERR_INVALID_ARG"

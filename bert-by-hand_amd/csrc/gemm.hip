@@ -17,7 +17,9 @@
 // global_load_lds_dwordx4 (16 bytes per lane, no register staging) into two
 // rings: the activations A, streamed from HBM, run SA-1 slices ahead (their
 // HBM latency is what a single shared ring exposes), the weights W, resident
-// in L2, one slice ahead; one barrier per slice.  Within a slice, row r is
+// in L2, SW-1 slices ahead (SW = 2 in every configuration in the table: deeper
+// W rings measured no faster); one barrier per slice.  The other pipeline
+// stages PD slices per thread in VGPRs and double-buffers one LDS tile.  Within a slice, row r is
 // 128 bytes = 8 chunks of 16 bytes and logical chunk c sits in slot
 // c ^ ((r >> 1) & 7): the 16 rows one MFMA operand fetch touches per LDS cycle
 // then hit 16 distinct bank groups.
@@ -61,9 +63,9 @@ enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
 constexpr size_t kLdsMax = 160 * 1024;
 
-template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0>
+template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0, int SW_ = 2>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SA = SA_, SW = 2, BK = 64;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SA = SA_, SW = SW_, BK = 64;
   static constexpr int PD = PD_;  // > 0: register prefetch depth (mainloop_reg)
   using L = Slice<64>;
   static constexpr int NW = WM * WN, THREADS = 64 * NW;  // 4 or 8 wavefronts
@@ -85,7 +87,12 @@ struct Cfg {
   static_assert(NW == 4 || NW == 8, "four or eight wavefronts");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is whole 32x32 blocks");
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load distribution");
-  static_assert(SA >= 2 && LA < 64, "A ring depth / vmcnt range");
+  static_assert(SA >= 2 && SW >= 2, "ring depths");
+  // vmcnt that may stay outstanding when slice kt must have landed: the
+  // copies issued after the later of W(kt) and A(kt) (W is issued first in
+  // each iteration).
+  static constexpr int VM_AHEAD = ((SA < SW ? SA : SW) - 2) * (LA + LW) + (SW < SA ? LA : 0);
+  static_assert(VM_AHEAD < 64, "vmcnt range");
   static_assert(LDS <= kLdsMax, "LDS");
   static_assert(PD == 0 || (BM * 8 % THREADS == 0 && BN * 8 % THREADS == 0), "chunks");
 };
@@ -121,8 +128,12 @@ __device__ __forceinline__ void interleave() {
 }
 
 // MFMA work of one 64-wide K slice staged in LDS (sA: BM rows, sW: BN rows).
-// Fragments are double-buffered across the four 16-wide k-steps and the
-// next step's LDS reads are spread over the current step's MFMAs.
+// The fragments of k-step s+PF are read from LDS while the MFMAs of step s
+// run (a ring of PF+1 fragment sets), so a step waits only for reads issued
+// PF steps earlier; the reads are spread over the MFMAs of a step.
+#ifndef BBH_LDS_PF
+#define BBH_LDS_PF 1  // 2 measured no faster and costs registers
+#endif
 template <class C>
 __device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
                                               f32x16 (&acc)[C::FM][C::FN]) {
@@ -132,7 +143,9 @@ __device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
   constexpr int KS = C::BK / 16;    // MFMA k-steps per slice
   constexpr int R = C::FM + C::FN;  // LDS fragment reads per k-step
   constexpr int Q = C::FM * C::FN;  // MFMAs per k-step
-  f16x8 a[2][C::FM], w[2][C::FN];
+  constexpr int PF = BBH_LDS_PF < KS ? BBH_LDS_PF : KS - 1;
+  constexpr int NB = PF + 1;
+  f16x8 a[NB][C::FM], w[NB][C::FN];
   auto rd = [&](int s, f16x8(&aa)[C::FM], f16x8(&ww)[C::FN]) {
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm)
@@ -141,18 +154,19 @@ __device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
     for (int fn = 0; fn < C::FN; ++fn)
       ww[fn] = *reinterpret_cast<const f16x8*>(sW + C::L::off(wn * C::TN + fn * 32 + r32, 2 * s + kh));
   };
-  rd(0, a[0], w[0]);
-  __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // all of step 0's reads first
+#pragma unroll
+  for (int p = 0; p < PF; ++p) rd(p, a[p], w[p]);
+  __builtin_amdgcn_sched_group_barrier(0x100, R * PF, 0);  // the first PF steps' reads first
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if (s + 1 < KS) rd(s + 1, a[(s + 1) & 1], w[(s + 1) & 1]);
+    if (s + PF < KS) rd(s + PF, a[(s + PF) % NB], w[(s + PF) % NB]);
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm)
 #pragma unroll
       for (int fn = 0; fn < C::FN; ++fn)
-        acc[fm][fn] = mfma32(w[s & 1][fn], a[s & 1][fm], acc[fm][fn]);
-    if (s + 1 < KS)
-      interleave<R, Q>();  // spread the next step's R fragment reads over these Q MFMAs
+        acc[fm][fn] = mfma32(w[s % NB][fn], a[s % NB][fm], acc[fm][fn]);
+    if (s + PF < KS)
+      interleave<R, Q>();  // spread step s+PF's R fragment reads over these Q MFMAs
     else
       __builtin_amdgcn_sched_group_barrier(0x008, Q, 0);
   }
@@ -187,25 +201,28 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
     issue_rows<C::BM, C::NW>(a0 + s * C::BK, K, M - m0, ringA + (s % C::SA) * C::A_STAGE);
   };
   auto issueW = [&](int s) {
-    issue_rows<C::BN, C::NW>(w0 + s * C::BK, K, C::BN, ringW + (s & 1) * C::W_STAGE);
+    issue_rows<C::BN, C::NW>(w0 + s * C::BK, K, C::BN, ringW + (s % C::SW) * C::W_STAGE);
   };
-  // prologue = iterations j = -(SA-1) .. -1 of the same schedule
+  // Slice s of W is issued SW-1 iterations and slice s of A SA-1 iterations
+  // before it is consumed; the prologue is iterations j = 1-max(SA,SW) .. -1
+  // of the same schedule.
+  constexpr int S = C::SA > C::SW ? C::SA : C::SW;
 #pragma unroll
-  for (int j = 1 - C::SA; j <= -1; ++j) {
-    if (j == -1) issueW(0);
-    if (j + C::SA - 1 < KT) issueA(j + C::SA - 1);
+  for (int j = 1 - S; j <= -1; ++j) {
+    if (j + C::SW - 1 >= 0 && j + C::SW - 1 < KT) issueW(j + C::SW - 1);
+    if (j + C::SA - 1 >= 0 && j + C::SA - 1 < KT) issueA(j + C::SA - 1);
   }
 
   for (int kt = 0; kt < KT; ++kt) {
-    if (C::SA >= 3 && kt + C::SA - 2 < KT)
-      wait_vm<C::LA>();
+    if (C::VM_AHEAD > 0 && kt + S - 2 < KT)
+      wait_vm<C::VM_AHEAD>();
     else
       wait_vm<0>();
     __syncthreads();  // slice kt visible to all; slice kt-1 fully consumed
-    if (kt + 1 < KT) issueW(kt + 1);
+    if (kt + C::SW - 1 < KT) issueW(kt + C::SW - 1);
     if (kt + C::SA - 1 < KT) issueA(kt + C::SA - 1);
     const f16* sA = ringA + (kt % C::SA) * C::A_STAGE;
-    const f16* sW = ringW + (kt & 1) * C::W_STAGE;
+    const f16* sW = ringW + (kt % C::SW) * C::W_STAGE;
     compute_slice<C>(sA, sW, acc);
   }
   __syncthreads();  // ring free for the epilogue
@@ -508,60 +525,61 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 //   27  128x192   64x96      PD 3   80 KB
 //   28  128x384   64x96 (8w) PD 2  128 KB   (owns whole rows)
 //   29  256x128   128x64     PD 3   96 KB
-// Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD>, epilogue>.
+// Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD,SW>, epilogue>.
 // The table itself: X(id, BM, BN, WM, WN, SA, PD), ids dense from 0.
-#define BBH_TILES(X)          \
-  X(0, 64, 64, 2, 2, 4, 0)    \
-  X(1, 64, 128, 2, 2, 4, 0)   \
-  X(2, 128, 64, 2, 2, 4, 0)   \
-  X(3, 128, 128, 2, 2, 4, 0)  \
-  X(4, 256, 128, 2, 2, 3, 0)  \
-  X(5, 128, 384, 1, 4, 4, 0)  \
-  X(6, 64, 384, 1, 4, 4, 0)   \
-  X(7, 32, 128, 1, 4, 4, 0)   \
-  X(8, 128, 192, 2, 2, 4, 0)  \
-  X(9, 256, 192, 2, 2, 3, 0)  \
-  X(10, 32, 384, 1, 4, 4, 0)  \
-  X(11, 128, 384, 1, 4, 3, 0) \
-  X(12, 256, 192, 2, 2, 2, 0) \
-  X(13, 128, 192, 2, 2, 3, 0) \
-  X(14, 64, 384, 1, 4, 2, 0)  \
-  X(15, 128, 128, 2, 2, 2, 0) \
-  X(16, 64, 128, 2, 2, 6, 0)  \
-  X(17, 256, 384, 2, 4, 2, 0) \
-  X(18, 128, 384, 2, 4, 4, 0) \
-  X(19, 256, 192, 4, 2, 3, 0) \
-  X(20, 256, 128, 4, 2, 3, 0) \
-  X(21, 128, 256, 2, 4, 4, 0) \
-  X(22, 128, 128, 2, 2, 2, 3) \
-  X(23, 128, 128, 2, 2, 2, 4) \
-  X(24, 128, 256, 2, 4, 2, 2) \
-  X(25, 256, 128, 4, 2, 2, 2) \
-  X(26, 64, 64, 2, 2, 2, 4)   \
-  X(27, 128, 192, 2, 2, 2, 3) \
-  X(28, 128, 384, 2, 4, 2, 2) \
-  X(29, 256, 128, 2, 2, 2, 3)
+// The table itself: X(id, BM, BN, WM, WN, SA, PD, SW), ids dense from 0.
+#define BBH_TILES(X) \
+  X(0, 64, 64, 2, 2, 4, 0, 2) \
+  X(1, 64, 128, 2, 2, 4, 0, 2) \
+  X(2, 128, 64, 2, 2, 4, 0, 2) \
+  X(3, 128, 128, 2, 2, 4, 0, 2) \
+  X(4, 256, 128, 2, 2, 3, 0, 2) \
+  X(5, 128, 384, 1, 4, 4, 0, 2) \
+  X(6, 64, 384, 1, 4, 4, 0, 2) \
+  X(7, 32, 128, 1, 4, 4, 0, 2) \
+  X(8, 128, 192, 2, 2, 4, 0, 2) \
+  X(9, 256, 192, 2, 2, 3, 0, 2) \
+  X(10, 32, 384, 1, 4, 4, 0, 2) \
+  X(11, 128, 384, 1, 4, 3, 0, 2) \
+  X(12, 256, 192, 2, 2, 2, 0, 2) \
+  X(13, 128, 192, 2, 2, 3, 0, 2) \
+  X(14, 64, 384, 1, 4, 2, 0, 2) \
+  X(15, 128, 128, 2, 2, 2, 0, 2) \
+  X(16, 64, 128, 2, 2, 6, 0, 2) \
+  X(17, 256, 384, 2, 4, 2, 0, 2) \
+  X(18, 128, 384, 2, 4, 4, 0, 2) \
+  X(19, 256, 192, 4, 2, 3, 0, 2) \
+  X(20, 256, 128, 4, 2, 3, 0, 2) \
+  X(21, 128, 256, 2, 4, 4, 0, 2) \
+  X(22, 128, 128, 2, 2, 2, 3, 2) \
+  X(23, 128, 128, 2, 2, 2, 4, 2) \
+  X(24, 128, 256, 2, 4, 2, 2, 2) \
+  X(25, 256, 128, 4, 2, 2, 2, 2) \
+  X(26, 64, 64, 2, 2, 2, 4, 2) \
+  X(27, 128, 192, 2, 2, 2, 3, 2) \
+  X(28, 128, 384, 2, 4, 2, 2, 2) \
+  X(29, 256, 128, 2, 2, 2, 3, 2)
 
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
                      const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
                      hipStream_t s) {
-#define BBH_CASE(ID, BM, BN, WM, WN, SA, PD)                                                 \
-  case ID:                                                                                 \
-    return launch<Cfg<BM, BN, WM, WN, SA, PD>, EPI>(A, W, bias, residual, gamma, beta, out, \
-                                                    M, N, K, eps, s);
+#define BBH_CASE(ID, BM, BN, WM, WN, SA, PD, SW)                                     \
+  case ID:                                                                           \
+    return launch<Cfg<BM, BN, WM, WN, SA, PD, SW>, EPI>(A, W, bias, residual, gamma, \
+                                                        beta, out, M, N, K, eps, s);
   switch (id) { BBH_TILES(BBH_CASE) }
 #undef BBH_CASE
   return hipErrorInvalidValue;
 }
 
-#define BBH_BN(ID, BM, BN, WM, WN, SA, PD) BN,
+#define BBH_BN(ID, BM, BN, WM, WN, SA, PD, SW) BN,
 constexpr int kBnOf[] = {BBH_TILES(BBH_BN)};
 #undef BBH_BN
 constexpr int kTiles = sizeof(kBnOf) / sizeof(kBnOf[0]);
 
-#define BBH_NAME(ID, BM, BN, WM, WN, SA, PD) \
-  "Cfg<" #BM "," #BN "," #WM "," #WN "," #SA "," #PD ">",
+#define BBH_NAME(ID, BM, BN, WM, WN, SA, PD, SW) \
+  "Cfg<" #BM "," #BN "," #WM "," #WN "," #SA "," #PD "," #SW ">",
 const char* const kTileName[] = {BBH_TILES(BBH_NAME)};
 #undef BBH_NAME
 

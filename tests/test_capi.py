@@ -153,8 +153,8 @@ def test_weight_view_entry_points_validate_before_launch():
 
 def test_tile_names_and_timing_arguments():
     L = _lib()
-    assert L.bbh_gemm_tile_name(23) == b"Cfg<128,128,2,2,2,4>"
-    assert L.bbh_gemm_tile_name(0) == b"Cfg<64,64,2,2,4,0>"
+    assert L.bbh_gemm_tile_name(23) == b"Cfg<128,128,2,2,2,4,2>"
+    assert L.bbh_gemm_tile_name(0) == b"Cfg<64,64,2,2,4,0,2>"
     assert L.bbh_gemm_tile_name(-1) == b"generic" and L.bbh_gemm_tile_name(999) == b"generic"
     cnt = ctypes.c_int(7)
     assert L.bbh_pool_timing(None, 16) == 1

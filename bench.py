@@ -280,9 +280,15 @@ def main():
             ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(64, seq))
             ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb), 300,
                        warmup=20)
+            # the same forward captured once as a HIP graph and replayed
+            graph = engine.EmbedGraph(ws, model, ids, types, mask, emb)
+            ms_g = timed(torch, graph.launch, 300, warmup=20)
+            graph.close()
             out[tag] = {"sentences_per_s": round(64 / (ms / 1e3), 1),
                         "ms_per_sentence": round(ms / 64, 6),
-                        "tflops": round(synth.flops_per_forward(64, seq) / (ms / 1e3) / 1e12, 2)}
+                        "tflops": round(synth.flops_per_forward(64, seq) / (ms / 1e3) / 1e12, 2),
+                        "graph_sentences_per_s": round(64 / (ms_g / 1e3), 1),
+                        "graph_ms_per_sentence": round(ms_g / 64, 6)}
             log(tag, out[tag])
         # ---- batch 256 x seq 512 ---------------------------------
         ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())

@@ -55,6 +55,9 @@ SIGNATURES = {
                           c_void_p]),
     "bbh_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                            c_void_p]),
+    "bbh_embed_graph_create": (c_int, [c_void_p] * 6 + [c_int, c_int, ctypes.POINTER(c_void_p)]),
+    "bbh_graph_launch": (c_int, [c_void_p, c_void_p]),
+    "bbh_graph_free": (c_int, [c_void_p]),
     "bbh_pool_create": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_void_p)]),
     "bbh_pool_free": (c_int, [c_void_p]),
     "bbh_embed_batches": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

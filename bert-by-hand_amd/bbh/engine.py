@@ -123,6 +123,35 @@ class _DeviceArray:
                                          "strides": None}
 
 
+class EmbedGraph:
+    """bert_embed on fixed device buffers, captured once as a HIP graph and
+    replayed with one launch (bbh_embed_graph_create / bbh_graph_launch)."""
+
+    def __init__(self, ws: "Workspace", w: "Model", ids, types, mask, emb):
+        _check_i32(ids, types, mask)
+        B, S = ids.shape
+        self.handle = ctypes.c_void_p()
+        self.emb = emb
+        self._keep = (ws, w, ids, types, mask, emb)  # the graph reads these buffers
+        call("bbh_embed_graph_create", ws.handle, w.handle, _ptr(ids), _ptr(types), _ptr(mask),
+             _ptr(emb), B, S, ctypes.byref(self.handle))
+
+    def launch(self, stream=None):
+        call("bbh_graph_launch", self.handle, _stream(stream))
+        return self.emb
+
+    def close(self):
+        if self.handle:
+            call("bbh_graph_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Pool:
     """n HIP streams, each with its own workspace; embed_batches overlaps
     independent batches across them (replaces a sequential batch loop)."""

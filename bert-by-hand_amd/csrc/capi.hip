@@ -460,11 +460,67 @@ bbh_status bbh_embed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
                      bbh_stream_t stream) {
   if (!ws || !m || !ids || !types || !mask || !emb)
     return fail(BBH_ERR_INVALID_ARG, "bbh_embed: null argument");
+  if (!aligned(emb, 4)) return misaligned("bbh_embed emb");
   BBH_TRY(check_shape(ws, batch, seq));
   const hipStream_t s = S(stream);
   BBH_TRY(run_encode(ws, m, ids, types, mask, ws->attn_out, batch, seq, s));
   return check_launch(bbh::pool_normalize(ws->attn_out, mask, static_cast<f16*>(emb), batch, seq, s),
                       "pool+normalize");
+}
+
+struct bbh_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+static void graph_release(bbh_graph* g) {
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
+bbh_status bbh_embed_graph_create(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                                  const int32_t* types, const int32_t* mask, void* emb, int batch,
+                                  int seq, bbh_graph** out) {
+  if (!out) return fail(BBH_ERR_INVALID_ARG, "null out");
+  *out = nullptr;
+  if (!ws || !m || !ids || !types || !mask || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed_graph_create: null argument");
+  if (!aligned(emb, 4)) return misaligned("bbh_embed_graph_create emb");
+  BBH_TRY(check_shape(ws, batch, seq));
+  hipStream_t s = nullptr;
+  BBH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  // One eager forward first: it validates the arguments and performs every
+  // kernel's one-time launch set-up outside the capture.
+  bbh_status st = bbh_embed(ws, m, ids, types, mask, emb, batch, seq, s);
+  hipError_t e = hipSuccess;
+  if (st == BBH_OK) e = hipStreamSynchronize(s);
+  auto* g = new bbh_graph();
+  if (st == BBH_OK && e == hipSuccess) e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (st == BBH_OK && e == hipSuccess) {
+    st = bbh_embed(ws, m, ids, types, mask, emb, batch, seq, s);
+    const hipError_t e2 = hipStreamEndCapture(s, &g->graph);  // ends the capture in every case
+    if (st == BBH_OK) e = e2;
+  }
+  if (st == BBH_OK && e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  (void)hipStreamDestroy(s);
+  if (st != BBH_OK || e != hipSuccess) {
+    graph_release(g);
+    return st != BBH_OK ? st : hip_fail(e, "graph capture");
+  }
+  *out = g;
+  return BBH_OK;
+}
+
+bbh_status bbh_graph_launch(bbh_graph* g, bbh_stream_t stream) {
+  if (!g || !g->exec) return fail(BBH_ERR_INVALID_ARG, "null graph");
+  BBH_HIP(hipGraphLaunch(g->exec, S(stream)), "hipGraphLaunch");
+  return BBH_OK;
+}
+
+bbh_status bbh_graph_free(bbh_graph* g) {
+  if (g) graph_release(g);
+  return BBH_OK;
 }
 
 bbh_status bbh_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,

@@ -123,6 +123,23 @@ bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
                       const int32_t *types, const int32_t *mask, void *out,
                       int batch, int seq, bbh_stream_t stream);
 
+/* ---- captured forwards ------------------------------------------------------
+ * For small batches a forward is bound by its ~44 kernel launches, not by the
+ * GPU (the reference notes the same at seq 16, README.md:113-116).
+ * bbh_embed_graph_create runs bbh_embed once on a private stream, then
+ * captures the same kernel sequence into a HIP graph; bbh_graph_launch
+ * replays the whole forward as one launch on `stream`.  The graph is bound to
+ * the buffers passed at creation (ids, types, mask, emb, the workspace and
+ * the model): refill the inputs in place between launches.  Creation
+ * synchronises its private stream; launches only enqueue.  Replays of one
+ * graph, and any other call on its workspace, must not overlap in time. */
+typedef struct bbh_graph bbh_graph;
+bbh_status bbh_embed_graph_create(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
+                                  const int32_t *types, const int32_t *mask, void *emb,
+                                  int batch, int seq, bbh_graph **out);
+bbh_status bbh_graph_launch(bbh_graph *g, bbh_stream_t stream);
+bbh_status bbh_graph_free(bbh_graph *g);
+
 /* ---- many batches ---------------------------------------------------------
  * A pool of n_streams HIP streams (default priority), each with its own
  * workspace of (max_batch, max_seq).  bbh_embed_batches runs bert_embed on

@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 42
+    assert len(names) == 45
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point
@@ -159,3 +159,14 @@ def test_tile_names_and_timing_arguments():
     cnt = ctypes.c_int(7)
     assert L.bbh_pool_timing(None, 16) == 1
     assert L.bbh_pool_timing_read(None, None, 0, ctypes.byref(cnt)) == 1
+
+
+def test_graph_entry_points_validate_before_touching_hip():
+    L = _lib()
+    g = ctypes.c_void_p()
+    fake = ctypes.c_void_p(256)
+    assert L.bbh_embed_graph_create(None, fake, fake, fake, fake, fake, 1, 16, ctypes.byref(g)) == 1
+    assert L.bbh_embed_graph_create(fake, fake, fake, fake, fake, ctypes.c_void_p(258), 1, 16,
+                                    ctypes.byref(g)) == 1  # emb not 4-byte aligned
+    assert L.bbh_graph_launch(None, None) == 1
+    assert L.bbh_graph_free(None) == 0

@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include <string>
+#include <algorithm>
 #include <vector>
 
 #include "../../include/bbh.h"
@@ -620,6 +621,8 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     int first, batch;
   };
   std::vector<Run> runs;
+  // A run holds at most a workspace's rows.  (Splitting long runs to even out
+  // the streams measured slower: smaller M costs more than the overlap gains.)
   const size_t cap = pool->ws[0]->rows;
   for (int i = 0; i < n_batches; ++i) {
     if (i > 0 && !runs.empty()) {
@@ -635,14 +638,27 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     }
     runs.push_back({i, batch_sizes[i]});
   }
+  // Largest run first onto the least-loaded stream (longest-processing-time
+  // order), so the streams finish together.
   const int n_runs = (int)runs.size();
+  std::vector<int> order(n_runs);
+  for (int r = 0; r < n_runs; ++r) order[r] = r;
+  auto rows_of = [&](int r) { return (size_t)runs[r].batch * seqs[runs[r].first]; };
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return rows_of(a) > rows_of(b); });
+  std::vector<size_t> load(n, 0);
+  std::vector<int> stream_of(n_runs);
+  for (int r : order) {
+    const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    stream_of[r] = j;
+    load[j] += rows_of(r);
+  }
   const hipStream_t caller = S(stream);
   BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
-  const int used = n_runs < n ? n_runs : n;
+  const int used = n_runs < n ? n_runs : n;  // streams with work: the first `used`
   for (int j = 0; j < used; ++j)
     BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
-  for (int r = 0; r < n_runs; ++r) {
-    const int j = r % n, i = runs[r].first, batch = runs[r].batch, seq = seqs[i];
+  for (int r : order) {
+    const int j = stream_of[r], i = runs[r].first, batch = runs[r].batch, seq = seqs[i];
     const int64_t o = tok_offsets[i];
     f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
     bbh_workspace* w = pool->ws[j];

@@ -124,15 +124,17 @@ bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
                       int batch, int seq, bbh_stream_t stream);
 
 /* ---- captured forwards ------------------------------------------------------
- * For small batches a forward is bound by its ~44 kernel launches, not by the
- * GPU (the reference notes the same at seq 16, README.md:113-116).
- * bbh_embed_graph_create runs bbh_embed once on a private stream, then
+ * One forward is ~44 kernel launches.  bbh_embed_graph_create runs bbh_embed
+ * once on a private stream, then
  * captures the same kernel sequence into a HIP graph; bbh_graph_launch
  * replays the whole forward as one launch on `stream`.  The graph is bound to
  * the buffers passed at creation (ids, types, mask, emb, the workspace and
  * the model): refill the inputs in place between launches.  Creation
  * synchronises its private stream; launches only enqueue.  Replays of one
- * graph, and any other call on its workspace, must not overlap in time. */
+ * graph, and any other call on its workspace, must not overlap in time.  This
+ * saves the host its per-kernel launch calls (for callers that capture or
+ * cannot afford them); on MI355X at batch 64 x seq 16 the GPU time per kernel
+ * dominates, and replays measure no faster than eager bbh_embed. */
 typedef struct bbh_graph bbh_graph;
 bbh_status bbh_embed_graph_create(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
                                   const int32_t *types, const int32_t *mask, void *emb,
@@ -143,8 +145,8 @@ bbh_status bbh_graph_free(bbh_graph *g);
 /* ---- many batches ---------------------------------------------------------
  * A pool of n_streams HIP streams (default priority), each with its own
  * workspace of (max_batch, max_seq).  bbh_embed_batches runs bert_embed on
- * n_batches batches, dealing them round-robin to the pool streams so that
- * independent batches overlap on the GPU; it replaces the reference's
+ * n_batches batches spread over the pool streams so that independent batches
+ * overlap on the GPU; it replaces the reference's
  * sequential corpus loop (bench/corpus.cu:64-77,120-132).  Batch i reads its
  * (batch_sizes[i], seqs[i]) ids/types/mask starting at element
  * tok_offsets[i] of the device arrays and writes batch_sizes[i] rows of emb
@@ -155,7 +157,8 @@ bbh_status bbh_graph_free(bbh_graph *g);
  * batches together gets larger kernels with every batch's padding unchanged
  * (the reference's corpus benchmark instead re-sorts sentences by length,
  * bench/corpus.cu:79-118).  Every sentence still gets the embedding it gets
- * alone, since sentences never interact.  The call orders itself after prior
+ * alone, since sentences never interact.  Runs go largest first to the
+ * least-loaded stream.  The call orders itself after prior
  * work on `stream` and makes later work on `stream` wait for all batches; it
  * returns without a host sync.  A pool must not be used by two overlapping
  * calls. */

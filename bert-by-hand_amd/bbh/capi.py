@@ -44,6 +44,7 @@ SIGNATURES = {
     "bbh_param_name": (c_char_p, [c_int]),
     "bbh_param_numel": (c_size_t, [c_int]),
     "bbh_model_load_dir": (c_int, [c_char_p, ctypes.POINTER(c_void_p)]),
+    "bbh_model_load_safetensors": (c_int, [c_char_p, ctypes.POINTER(c_void_p)]),
     "bbh_model_from_host": (c_int, [ctypes.POINTER(c_void_p), c_int, ctypes.POINTER(c_void_p)]),
     "bbh_model_free": (c_int, [c_void_p]),
     "bbh_model_device_bytes": (c_size_t, [c_void_p]),

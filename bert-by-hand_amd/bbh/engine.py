@@ -72,6 +72,12 @@ class Model:
         call("bbh_model_load_dir", directory.encode(), ctypes.byref(h))
         return cls(h)
 
+    @classmethod
+    def load_safetensors(cls, path: str) -> "Model":
+        h = ctypes.c_void_p()
+        call("bbh_model_load_safetensors", path.encode(), ctypes.byref(h))
+        return cls(h)
+
     def close(self):
         if self.handle:
             call("bbh_model_free", self.handle)

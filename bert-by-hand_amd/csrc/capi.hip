@@ -12,6 +12,7 @@
 // pool+normalize launch after them: 32 launches per bert_embed against the
 // reference's 58 launches and a device-to-device copy (src/model/forward.cu).
 
+#include <ctype.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -20,6 +21,7 @@
 
 #include <string>
 #include <algorithm>
+#include <map>
 #include <vector>
 
 #include "../../include/bbh.h"
@@ -50,30 +52,33 @@ bbh_status hip_fail(hipError_t e, const char* what) {
 struct Param {
   std::string name;
   size_t numel;
+  size_t rows = 0;  // 2-D tensors: the (out) row count; 0 for vectors
 };
 
 const std::vector<Param>& params() {
   static const std::vector<Param> p = [] {
     std::vector<Param> v;
     const size_t H = BBH_HIDDEN, F = BBH_FFN_DIM;
-    v.push_back({"embeddings.word_embeddings.weight", (size_t)BBH_VOCAB_SIZE * H});
-    v.push_back({"embeddings.position_embeddings.weight", (size_t)BBH_MAX_POSITION * H});
-    v.push_back({"embeddings.token_type_embeddings.weight", (size_t)BBH_TYPE_VOCAB_SIZE * H});
+    v.push_back({"embeddings.word_embeddings.weight", (size_t)BBH_VOCAB_SIZE * H, BBH_VOCAB_SIZE});
+    v.push_back({"embeddings.position_embeddings.weight", (size_t)BBH_MAX_POSITION * H,
+                 BBH_MAX_POSITION});
+    v.push_back({"embeddings.token_type_embeddings.weight", (size_t)BBH_TYPE_VOCAB_SIZE * H,
+                 BBH_TYPE_VOCAB_SIZE});
     v.push_back({"embeddings.LayerNorm.weight", H});
     v.push_back({"embeddings.LayerNorm.bias", H});
     for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
       const std::string p = "encoder.layer." + std::to_string(i) + ".";
       for (const char* part : {"query", "key", "value"}) {
-        v.push_back({p + "attention.self." + part + ".weight", H * H});
+        v.push_back({p + "attention.self." + part + ".weight", H * H, H});
         v.push_back({p + "attention.self." + part + ".bias", H});
       }
-      v.push_back({p + "attention.output.dense.weight", H * H});
+      v.push_back({p + "attention.output.dense.weight", H * H, H});
       v.push_back({p + "attention.output.dense.bias", H});
       v.push_back({p + "attention.output.LayerNorm.weight", H});
       v.push_back({p + "attention.output.LayerNorm.bias", H});
-      v.push_back({p + "intermediate.dense.weight", F * H});
+      v.push_back({p + "intermediate.dense.weight", F * H, F});
       v.push_back({p + "intermediate.dense.bias", F});
-      v.push_back({p + "output.dense.weight", H * F});
+      v.push_back({p + "output.dense.weight", H * F, H});
       v.push_back({p + "output.dense.bias", H});
       v.push_back({p + "output.LayerNorm.weight", H});
       v.push_back({p + "output.LayerNorm.bias", H});
@@ -387,6 +392,236 @@ bbh_status bbh_model_load_dir(const char* dir, bbh_model** out) {
     if (got != p[i].numel)
       return fail(BBH_ERR_IO, path + ": short read (" + std::to_string(got) + " of " +
                                   std::to_string(p[i].numel) + " elements)");
+  }
+  return model_from_host_blob(host, out);
+}
+
+// ---- safetensors ------------------------------------------------------------
+// The container (huggingface/safetensors): an 8-byte little-endian header
+// length N, N bytes of JSON mapping each tensor name to
+// {"dtype", "shape", "data_offsets": [begin, end)} (offsets into the data
+// section that follows the header), plus an optional "__metadata__" object.
+namespace {
+
+struct StTensor {
+  std::string dtype;
+  std::vector<int64_t> shape;
+  int64_t begin = -1, end = -1;
+};
+
+// Just enough JSON for that header: objects, arrays, strings, integers and
+// the literals; any other value is skipped structurally.
+class Json {
+ public:
+  explicit Json(const std::string& s) : s_(s) {}
+  bool ok() const { return ok_; }
+  bool eat(char c) {
+    ws();
+    if (i_ < s_.size() && s_[i_] == c) {
+      ++i_;
+      return true;
+    }
+    return false;
+  }
+  bool expect(char c) {
+    if (!eat(c)) ok_ = false;
+    return ok_;
+  }
+  std::string str() {
+    std::string out;
+    if (!expect('"')) return out;
+    while (i_ < s_.size() && s_[i_] != '"') {
+      char ch = s_[i_++];
+      if (ch == '\\') {
+        if (i_ >= s_.size()) break;
+        const char e = s_[i_++];
+        if (e == 'u') {  // \uXXXX: tensor names are ASCII; keep a placeholder
+          i_ += 4;
+          ch = '?';
+        } else {
+          ch = e == 'n' ? '\n' : e == 't' ? '\t' : e == 'r' ? '\r' : e == 'b' ? '\b' : e == 'f' ? '\f' : e;
+        }
+      }
+      out += ch;
+    }
+    if (i_ > s_.size() || !eat('"')) ok_ = false;
+    return out;
+  }
+  int64_t integer() {
+    ws();
+    size_t j = i_;
+    const bool neg = j < s_.size() && s_[j] == '-';
+    if (neg) ++j;
+    int64_t v = 0;
+    const size_t start = j;
+    while (j < s_.size() && s_[j] >= '0' && s_[j] <= '9' && v < ((int64_t)1 << 56))
+      v = v * 10 + (s_[j++] - '0');
+    if (j == start) ok_ = false;
+    i_ = j;
+    return neg ? -v : v;
+  }
+  void skip(int depth = 0) {  // any value
+    ws();
+    if (!ok_ || i_ >= s_.size() || depth > 64) {
+      ok_ = false;
+      return;
+    }
+    const char c = s_[i_];
+    if (c == '"') {
+      str();
+    } else if (c == '{' || c == '[') {
+      const char close = c == '{' ? '}' : ']';
+      ++i_;
+      if (eat(close)) return;
+      do {
+        if (c == '{') {
+          str();
+          expect(':');
+        }
+        skip(depth + 1);
+      } while (ok_ && eat(','));
+      expect(close);
+    } else {  // number or literal
+      while (i_ < s_.size() && (isalnum((unsigned char)s_[i_]) || s_[i_] == '-' || s_[i_] == '+' ||
+                                s_[i_] == '.'))
+        ++i_;
+    }
+  }
+
+ private:
+  void ws() {
+    while (i_ < s_.size() && isspace((unsigned char)s_[i_])) ++i_;
+  }
+  const std::string& s_;
+  size_t i_ = 0;
+  bool ok_ = true;
+};
+
+bool parse_st_header(const std::string& js, std::map<std::string, StTensor>& out) {
+  Json j(js);
+  if (!j.expect('{')) return false;
+  if (j.eat('}')) return true;
+  do {
+    const std::string key = j.str();
+    if (!j.expect(':')) return false;
+    if (key == "__metadata__") {
+      j.skip();
+      continue;
+    }
+    StTensor t;
+    if (!j.expect('{')) return false;
+    if (!j.eat('}')) {
+      do {
+        const std::string k = j.str();
+        if (!j.expect(':')) return false;
+        if (k == "dtype") {
+          t.dtype = j.str();
+        } else if (k == "shape") {
+          if (!j.expect('[')) return false;
+          if (!j.eat(']')) {
+            do t.shape.push_back(j.integer());
+            while (j.ok() && j.eat(','));
+            if (!j.expect(']')) return false;
+          }
+        } else if (k == "data_offsets") {
+          if (!j.expect('[')) return false;
+          t.begin = j.integer();
+          if (!j.expect(',')) return false;
+          t.end = j.integer();
+          if (!j.expect(']')) return false;
+        } else {
+          j.skip();
+        }
+      } while (j.ok() && j.eat(','));
+      if (!j.expect('}')) return false;
+    }
+    out[key] = t;
+  } while (j.ok() && j.eat(','));
+  return j.expect('}') && j.ok();
+}
+
+// IEEE binary16 bits of a float, round to nearest even (the host compiler's
+// _Float16 conversion), and of a bfloat16 via its float value.
+uint16_t f32_to_f16_bits(float v) {
+  const _Float16 h = (_Float16)v;
+  uint16_t b;
+  memcpy(&b, &h, 2);
+  return b;
+}
+
+}  // namespace
+
+bbh_status bbh_model_load_safetensors(const char* path, bbh_model** out) {
+  if (!path || !out) return fail(BBH_ERR_INVALID_ARG, "null path/out");
+  FILE* f = fopen(path, "rb");
+  if (!f) return fail(BBH_ERR_IO, std::string("cannot open ") + path);
+  struct Closer {
+    FILE* f;
+    ~Closer() { fclose(f); }
+  } closer{f};
+  fseek(f, 0, SEEK_END);
+  const long fsz = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  unsigned char lenb[8];
+  if (fsz < 8 || fread(lenb, 1, 8, f) != 8)
+    return fail(BBH_ERR_IO, std::string(path) + ": not a safetensors file (no header length)");
+  uint64_t hlen = 0;
+  for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | lenb[i];
+  if (hlen == 0 || hlen > (100u << 20) || 8 + hlen > (uint64_t)fsz)
+    return fail(BBH_ERR_IO, std::string(path) + ": bad header length " + std::to_string(hlen));
+  std::string header(hlen, '\0');
+  if (fread(&header[0], 1, hlen, f) != hlen)
+    return fail(BBH_ERR_IO, std::string(path) + ": short header");
+  std::map<std::string, StTensor> tensors;
+  if (!parse_st_header(header, tensors))
+    return fail(BBH_ERR_IO, std::string(path) + ": malformed header JSON");
+  const uint64_t data_size = (uint64_t)fsz - 8 - hlen;
+
+  const auto& p = params();
+  const BlobLayout& L = layout();
+  std::vector<uint16_t> host(L.total, 0);
+  std::vector<unsigned char> buf;
+  for (size_t i = 0; i < p.size(); ++i) {
+    auto it = tensors.find(p[i].name);
+    if (it == tensors.end()) it = tensors.find("bert." + p[i].name);
+    if (it == tensors.end())
+      return fail(BBH_ERR_IO, std::string(path) + ": missing tensor " + p[i].name);
+    const StTensor& t = it->second;
+    const std::string where = std::string(path) + ": " + it->first;
+    const size_t esz = t.dtype == "F32" ? 4 : (t.dtype == "F16" || t.dtype == "BF16") ? 2 : 0;
+    if (esz == 0) return fail(BBH_ERR_IO, where + ": dtype " + t.dtype + " (want F32, F16 or BF16)");
+    const std::vector<int64_t> want =
+        p[i].rows ? std::vector<int64_t>{(int64_t)p[i].rows, (int64_t)(p[i].numel / p[i].rows)}
+                  : std::vector<int64_t>{(int64_t)p[i].numel};
+    if (t.shape != want) {
+      std::string got;
+      for (auto d : t.shape) got += (got.empty() ? "" : ",") + std::to_string(d);
+      return fail(BBH_ERR_IO, where + ": shape [" + got + "]");
+    }
+    if (t.begin < 0 || t.end < t.begin || (uint64_t)t.end > data_size ||
+        (uint64_t)(t.end - t.begin) != p[i].numel * esz)
+      return fail(BBH_ERR_IO, where + ": data_offsets out of range or wrong size");
+    buf.resize(p[i].numel * esz);
+    if (fseek(f, (long)(8 + hlen + t.begin), SEEK_SET) != 0 ||
+        fread(buf.data(), 1, buf.size(), f) != buf.size())
+      return fail(BBH_ERR_IO, where + ": short read");
+    uint16_t* dst = host.data() + L.off[i];
+    if (t.dtype == "F16") {
+      memcpy(dst, buf.data(), buf.size());
+    } else if (t.dtype == "F32") {
+      for (size_t e = 0; e < p[i].numel; ++e) {
+        float v;
+        memcpy(&v, buf.data() + 4 * e, 4);
+        dst[e] = f32_to_f16_bits(v);
+      }
+    } else {  // BF16: the upper half of a float
+      for (size_t e = 0; e < p[i].numel; ++e) {
+        const uint32_t bits = (uint32_t)(buf[2 * e] | (buf[2 * e + 1] << 8)) << 16;
+        float v;
+        memcpy(&v, &bits, 4);
+        dst[e] = f32_to_f16_bits(v);
+      }
+    }
   }
   return model_from_host_blob(host, out);
 }

@@ -89,6 +89,14 @@ bbh_status bbh_model_load_dir(const char *dir, bbh_model **out);
  * binary16 values of tensor bbh_param_name(i). */
 bbh_status bbh_model_from_host(const uint16_t *const *tensors, int n_tensors,
                                bbh_model **out);
+/* The same model from a Hugging Face safetensors file (the model.safetensors
+ * of a BertModel / sentence-transformers checkpoint; the reference exports the
+ * same state dict to .bin files, scripts/dump_weights.py:69-94).  Tensors
+ * named as above, optionally prefixed "bert."; dtype F32, F16 or BF16,
+ * converted to fp16 with round-to-nearest-even; other tensors (the pooler)
+ * are ignored.  Every tensor is found and checked (dtype, exact shape, byte
+ * range) before any device memory is touched. */
+bbh_status bbh_model_load_safetensors(const char *path, bbh_model **out);
 bbh_status bbh_model_free(bbh_model *m);
 size_t bbh_model_device_bytes(const bbh_model *m);
 

@@ -277,3 +277,36 @@ def test_embed_graph_replays_match_eager(torch_cuda, ws, model):
         assert np.array_equal(got, want), rep
     g.close()
     ws2.close()
+
+
+def test_load_safetensors_equals_from_host(torch_cuda, ws, model, weights32, tmp_path,
+                                           golden_model):
+    # fp32 file with plain names, fp16 file with the "bert." prefix and a pooler
+    # tensor: both give the model bbh_model_from_host gives (same fp16 bits,
+    # same embeddings); a bf16 file stays within bf16 rounding of the oracle.
+    stn = pytest.importorskip("safetensors.numpy")
+    from bbh import engine
+
+    g = golden_model
+    want = _embed(torch_cuda, ws, model, g["rag_ids"], g["rag_types"], g["rag_mask"])
+    files = {
+        "f32": {k: v.astype(np.float32) for k, v in weights32.items()},
+        "f16": {"bert." + k: v.astype(np.float16) for k, v in weights32.items()},
+    }
+    files["f16"]["bert.pooler.dense.weight"] = np.zeros((384, 384), np.float16)
+    for tag, d in files.items():
+        path = str(tmp_path / f"{tag}.safetensors")
+        stn.save_file(d, path)
+        m2 = engine.Model.load_safetensors(path)
+        got = _embed(torch_cuda, ws, m2, g["rag_ids"], g["rag_types"], g["rag_mask"])
+        m2.close()
+        assert np.array_equal(got, want), tag
+    import torch
+    from safetensors.torch import save_file
+
+    path = str(tmp_path / "bf16.safetensors")
+    save_file({k: torch.from_numpy(v).to(torch.bfloat16) for k, v in weights32.items()}, path)
+    m3 = engine.Model.load_safetensors(path)
+    got = _embed(torch_cuda, ws, m3, g["rag_ids"], g["rag_types"], g["rag_mask"])
+    m3.close()
+    assert cosine_rows(got, g["rag_embedding"]).min() >= 0.999

@@ -115,6 +115,40 @@ def cpu_baseline(batches, weights, budget_s=12.0):
                       f"({n_sent} sentences) of the varlen mix, {dt:.1f} s"}
 
 
+def tokenizer_rate(engine, synth, n=2000, seq=128, reps=5):
+    """Host-side text -> ids throughput of the WordPiece tokenizer on seeded
+    synthetic texts and vocabulary (one thread), beside transformers'
+    BertTokenizerFast (the reference's tokenizer; Rust, batch-parallel) on
+    the same texts when it is importable."""
+    import tempfile
+
+    vocab, texts = synth.text_vocab(), synth.texts(seed=3, n=n)
+    out = {"texts": n, "seq": seq, "threads": 1, "vocab": f"seeded synthetic ({len(vocab)} entries)"}
+    with tempfile.TemporaryDirectory() as d:
+        with open(os.path.join(d, "vocab.txt"), "w", encoding="utf-8") as f:
+            f.write("\n".join(vocab) + "\n")
+        tok = engine.Tokenizer(os.path.join(d, "vocab.txt"))
+        tok(texts[:100], seq)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            tok(texts, seq)
+        out["sentences_per_s"] = round(n * reps / (time.perf_counter() - t0), 1)
+        tok.close()
+        try:
+            import transformers
+
+            ref = transformers.BertTokenizerFast.from_pretrained(d, do_lower_case=True)
+            kw = dict(padding="max_length", truncation=True, max_length=seq, return_tensors="np")
+            ref(texts[:100], **kw)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                ref(texts, **kw)
+            out["hf_bert_tokenizer_fast_sentences_per_s"] = round(n * reps / (time.perf_counter() - t0), 1)
+        except Exception as e:  # pragma: no cover
+            out["hf_bert_tokenizer_fast_sentences_per_s"] = f"unavailable ({type(e).__name__})"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,6 +344,10 @@ def main():
             "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
             "per_gemm_frac": gem}
         log("cfg5", out["cfg5_b256_s512"])
+
+    if not args.no_extras:
+        out["tokenizer"] = tokenizer_rate(engine, synth)
+        log("tokenizer", out["tokenizer"])
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(batches, weights)

@@ -97,6 +97,11 @@ SIGNATURES = {
     "bbh_l2_normalize": (c_int, [c_void_p, c_int, c_int, c_void_p]),
     "bbh_pool_normalize": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "bbh_gelu": (c_int, [c_void_p, c_int, c_void_p]),
+    "bbh_tokenizer_load": (c_int, [c_char_p, c_int, ctypes.POINTER(c_void_p)]),
+    "bbh_tokenizer_free": (c_int, [c_void_p]),
+    "bbh_tokenizer_vocab_size": (c_int, [c_void_p]),
+    "bbh_tokenize": (c_int, [c_void_p, ctypes.POINTER(c_char_p), c_int, c_int, c_void_p, c_void_p,
+                             c_void_p, c_void_p]),
 }
 
 STATUS = {

@@ -393,6 +393,40 @@ def launch_pool_normalize(hidden, mask, out, seq, batch=1, stream=None):
     return out
 
 
+class Tokenizer:
+    """The uncased BERT WordPiece tokenizer (bbh_tokenizer_load / bbh_tokenize):
+    texts -> host int32 (n, seq) ids, types, mask, as
+    BertTokenizerFast(..., padding="max_length", truncation=True) gives."""
+
+    def __init__(self, vocab_path: str, lowercase: bool = True):
+        self.handle = ctypes.c_void_p()
+        call("bbh_tokenizer_load", vocab_path.encode(), int(lowercase), ctypes.byref(self.handle))
+
+    @property
+    def vocab_size(self) -> int:
+        return lib().bbh_tokenizer_vocab_size(self.handle)
+
+    def __call__(self, texts, seq: int = 128):
+        n = len(texts)
+        arr = (ctypes.c_char_p * max(n, 1))(*[t.encode("utf-8") for t in texts])
+        ids, types, mask = (np.zeros((n, seq), np.int32) for _ in range(3))
+        lengths = np.zeros(n, np.int32)
+        p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+        call("bbh_tokenize", self.handle, arr, n, seq, p(ids), p(types), p(mask), p(lengths))
+        return ids, types, mask, lengths
+
+    def close(self):
+        if self.handle:
+            call("bbh_tokenizer_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def gemm_tile_name(tile: int) -> str:
     """Template argument of the GEMM kernel symbol for a tile id."""
     return capi.lib().bbh_gemm_tile_name(tile).decode()

@@ -179,3 +179,73 @@ def flops_per_forward(batch: int, seq: int) -> int:
     gemm = NUM_LAYERS * 2 * (HIDDEN * 3 * HIDDEN + HIDDEN * HIDDEN + 2 * HIDDEN * FFN_DIM)
     attn = NUM_LAYERS * 4 * NUM_HEADS * HEAD_DIM
     return batch * seq * gemm + batch * attn * seq * seq
+
+
+# --------------------------------------------------------------------------
+# text (tokenizer tests and timing)
+# --------------------------------------------------------------------------
+
+TEXT_WORDS = ("the a of and to in is was for on with as by at from that this it be are "
+         "hello world model token embed sentence vector gpu kernel matrix batch layer "
+         "attention learning deep neural network fast slow big small red blue green "
+         "café naïve résumé über straße mañana ελληνικά русский язык").split()
+
+
+def text_vocab(seed: int = 0) -> list:
+    """A seeded WordPiece vocabulary (specials, characters, ## pieces, the
+    TEXT_WORDS and their subword pieces) for tokenizer tests and timing; the
+    real MiniLM vocab.txt is not available offline."""
+    rng = np.random.default_rng(seed)
+    toks = ["[PAD]", "[UNK]", "[CLS]", "[SEP]", "[MASK]"]
+    chars = [chr(c) for c in range(33, 127)] + list("αβγδεζηθλμπσςωабвгдежзиклмн中文字词语日本語한국어") \
+        + ["ᄀ", "ᅡ", "ᆨ", "ᄒ", "ᅩ"]
+    toks += [c.lower() for c in chars]
+    toks += ["##" + c.lower() for c in chars if c.isalnum()]
+    for w in TEXT_WORDS:
+        w = w.lower()
+        toks.append(w)
+        for k in range(2, len(w)):  # subword pieces of every word
+            if rng.random() < 0.5:
+                toks.append("##" + w[k:])
+            if rng.random() < 0.3:
+                toks.append(w[:k])
+    for _ in range(400):  # random pieces
+        n = int(rng.integers(2, 6))
+        s = "".join(rng.choice(list("abcdefghijklmnopqrstuvwxyz"), n))
+        toks.append(("##" if rng.random() < 0.5 else "") + s)
+    seen, vocab = set(), []
+    for t in toks:
+        if t not in seen:
+            seen.add(t)
+            vocab.append(t)
+    return vocab
+
+
+def texts(seed: int = 1, n: int = 400) -> list:
+    """Seeded synthetic sentences over TEXT_WORDS, punctuation and a set of
+    Unicode edge cases (each also appended alone)."""
+    rng = np.random.default_rng(seed)
+    extra = ["中文", "日本語です", "한국어", "Ωmega", "ÅNGSTRÖM", "Ǆ", "İstanbul", "ß", "ΣΑΣ",
+             "emoji 🙂👍", "zero​width", "tab\there", "nl\nline", "nbsp x",
+             "ideo　space", "ctl\x07bell", "\x0bvt", "soft­hyphen", "x" * 120,
+             "unk§¶word", "dashes—and–more", "quote«»„“", "num3r1c 42 3.14", "a.b,c;d:e!f?g",
+             "[cls] lower", "[CLS][SEP]x[MASK]y", "[UNK", "e\u0301te", "A\u030Angstrom",
+             "1+1=2 <tag> a|b ~x ^y `z", "price 5€ ©2024 ™", "ｆｕｌｌｗｉｄｔｈ", "ﬁne ligature",
+             "\u0915\u094D\u0937", "mixed中文and한글text"]
+    texts = []
+    for _ in range(n):
+        k = int(rng.integers(1, 25))
+        parts = []
+        for _ in range(k):
+            r = rng.random()
+            if r < 0.6:
+                w = rng.choice(TEXT_WORDS)
+                parts.append(w.upper() if rng.random() < 0.2 else w.capitalize() if rng.random() < 0.3 else w)
+            elif r < 0.8:
+                parts.append(str(rng.choice(list(",.!?;:'\"()-"))))
+            else:
+                parts.append(str(rng.choice(extra)))
+        sep = " " if rng.random() < 0.8 else "  \t"
+        texts.append(sep.join(parts))
+    texts += ["", "   ", "[CLS] literal", "Hello, World!"] + extra  # every case at least once
+    return texts

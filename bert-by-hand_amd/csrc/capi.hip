@@ -38,6 +38,16 @@ bbh_status fail(bbh_status s, const std::string& msg) {
   return s;
 }
 
+}  // namespace
+
+// The thread's last-error message, for the library's other host sources
+// (tokenizer.cpp).
+namespace bbh_detail {
+bbh_status set_error(bbh_status s, const std::string& msg) { return fail(s, msg); }
+}  // namespace bbh_detail
+
+namespace {
+
 bbh_status hip_fail(hipError_t e, const char* what) {
   return fail(BBH_ERR_HIP, std::string(what) + ": " + hipGetErrorName(e) + " (" +
                                hipGetErrorString(e) + ")");

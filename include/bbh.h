@@ -324,6 +324,27 @@ bbh_status bbh_pool_normalize(const void *hidden, const int32_t *mask, void *out
  * epilogue; this entry point is the standalone operator. */
 bbh_status bbh_gelu(void *x, int n, bbh_stream_t stream);
 
+/* ---- text -> ids (WordPiece) -------------------------------------------------
+ * The uncased BERT tokenizer the reference calls through sentence-transformers
+ * (Hugging Face tokenizers' BertTokenizerFast, scripts/dump_weights.py:100-106,
+ * scripts/dump_corpus.py:34-39, padding="max_length", truncation=True): clean
+ * text, CJK ideographs split, accents stripped and text lowercased (when
+ * `lowercase`), split on whitespace and punctuation, greedy longest-match
+ * WordPiece with "##" continuations and [UNK] for words over 100 characters or
+ * without a match.  vocab.txt holds one token per line, id = line number; it
+ * must contain [CLS], [SEP], [PAD] and [UNK].  Host-side only: the outputs are
+ * host arrays ready to copy to the device. */
+typedef struct bbh_tokenizer bbh_tokenizer;
+bbh_status bbh_tokenizer_load(const char *vocab_path, int lowercase, bbh_tokenizer **out);
+bbh_status bbh_tokenizer_free(bbh_tokenizer *t);
+int bbh_tokenizer_vocab_size(const bbh_tokenizer *t);
+/* n NUL-terminated UTF-8 texts -> ids / types / mask, each (n, seq) int32
+ * row-major: [CLS] tokens [SEP] [PAD]..., tokens truncated to seq - 2; types
+ * 0; mask 1 on [CLS], tokens and [SEP].  lengths (optional, n entries) gets
+ * each row's unpadded length.  Malformed UTF-8 bytes are dropped.  seq >= 2. */
+bbh_status bbh_tokenize(const bbh_tokenizer *t, const char *const *texts, int n, int seq,
+                        int32_t *ids, int32_t *types, int32_t *mask, int32_t *lengths);
+
 #ifdef __cplusplus
 }
 #endif

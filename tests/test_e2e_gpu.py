@@ -310,3 +310,20 @@ def test_load_safetensors_equals_from_host(torch_cuda, ws, model, weights32, tmp
     got = _embed(torch_cuda, ws, m3, g["rag_ids"], g["rag_types"], g["rag_mask"])
     m3.close()
     assert cosine_rows(got, g["rag_embedding"]).min() >= 0.999
+
+
+def test_text_to_embedding(torch_cuda, ws, model, weights32, tmp_path):
+    # text -> bbh_tokenize -> bbh_embed, against the oracle on the same ids
+    from bbh import engine, synth
+
+    vocab = synth.text_vocab()
+    path = tmp_path / "vocab.txt"
+    path.write_text("\n".join(vocab) + "\n", encoding="utf-8")
+    tok = engine.Tokenizer(str(path))
+    texts = synth.texts(seed=5, n=40)
+    ids, types, mask, lens = tok(texts, 64)
+    tok.close()
+    assert ids.shape == (len(texts), 64) and lens.min() >= 2
+    got = _embed(torch_cuda, ws, model, ids, types, mask)
+    want = O.bert_embed(weights32, ids, types, mask)
+    assert cosine_rows(got, want).min() >= COS

@@ -59,6 +59,17 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Workgroup barrier over LDS: this wave's LDS operations complete
+// (lgkmcnt 0), then s_barrier.  __syncthreads() also carries a workgroup
+// release fence, which compiles to s_waitcnt vmcnt(0): it would drain every
+// global->LDS copy and register prefetch issued for later slices at each
+// slice, leaving the rings no lookahead.  The K loops wait for exactly the
+// copies a slice needs (wait_vm) before this barrier.  The memory clobber keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
 constexpr size_t kLdsMax = 160 * 1024;
@@ -218,14 +229,14 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
       wait_vm<C::VM_AHEAD>();
     else
       wait_vm<0>();
-    __syncthreads();  // slice kt visible to all; slice kt-1 fully consumed
+    lds_barrier();  // slice kt visible to all; slice kt-1 fully consumed
     if (kt + C::SW - 1 < KT) issueW(kt + C::SW - 1);
     if (kt + C::SA - 1 < KT) issueA(kt + C::SA - 1);
     const f16* sA = ringA + (kt % C::SA) * C::A_STAGE;
     const f16* sW = ringW + (kt % C::SW) * C::W_STAGE;
     compute_slice<C>(sA, sW, acc);
   }
-  __syncthreads();  // ring free for the epilogue
+  lds_barrier();  // ring free for the epilogue
 }
 
 // The K loop with register staging: each thread keeps the 16-byte chunks of
@@ -284,13 +295,13 @@ __device__ __forceinline__ void mainloop_reg(const f16* __restrict__ A,
       if (kt < KT) {
         store(kt & 1, ra[d], rw[d]);
         if (kt + D < KT) load(kt + D, ra[d], rw[d]);
-        __syncthreads();
+        lds_barrier();
         const f16* sA = smem + (kt & 1) * (C::A_STAGE + C::W_STAGE);
         compute_slice<C>(sA, sA + C::A_STAGE, acc);
       }
     }
   }
-  __syncthreads();  // LDS free for the epilogue
+  lds_barrier();  // LDS free for the epilogue
 }
 
 // Tile coordinates from the workgroup id, XCD-aware (see header).
@@ -305,13 +316,25 @@ __device__ __forceinline__ bool tile_of(int nb, int mb, int& mi, int& ni) {
 // to C rows m0.. with 16-byte stores.
 template <class C, int ROWS>
 __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ out, int ldc, int M,
-                                           int m0, int n0) {
+                                           int m0, int n0, const f16* residual) {
   constexpr int CPR = C::BN / 8;
-  for (int idx = threadIdx.x; idx < ROWS * CPR; idx += C::THREADS) {
+  constexpr int PER = (ROWS * CPR + C::THREADS - 1) / C::THREADS;
+  // Unrolled so the residual loads of several rows are in flight together
+  // (by 4 when the tile is staged in passes and other accumulators are live).
+#pragma unroll(C::NPASS == 1 ? PER : 4)
+  for (int q = 0; q < PER; ++q) {
+    const int idx = threadIdx.x + q * C::THREADS;
     const int r = idx / CPR, c = idx % CPR;
-    if (m0 + r < M)
-      *reinterpret_cast<f16x8*>(out + (size_t)(m0 + r) * ldc + n0 + c * 8) =
-          *reinterpret_cast<const f16x8*>(tile + r * C::OUT_LD + c * 8);
+    if (idx < ROWS * CPR && m0 + r < M) {
+      f16x8 v = *reinterpret_cast<const f16x8*>(tile + r * C::OUT_LD + c * 8);
+      if (residual) {
+        const f16x8 rv =
+            *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + r) * ldc + n0 + c * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (f16)((float)v[i] + (float)rv[i]);
+      }
+      *reinterpret_cast<f16x8*>(out + (size_t)(m0 + r) * ldc + n0 + c * 8) = v;
+    }
   }
 }
 
@@ -338,23 +361,67 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   float* red = reinterpret_cast<float*>(smem + PR * C::OUT_LD);  // [2][WN][BM]
   float mean[C::FM], rstd[C::FM];
 
+  // Per-column operands (bias; gamma and beta for LayerNorm) depend only on
+  // the lane's columns.  Tiles with room in registers load them once, all
+  // together, so their latency is paid once per tile instead of once per
+  // 32x32 block; the 192-accumulator tiles load them once per column block.
+  constexpr bool kHoist = C::FM * C::FN <= 8;
+  constexpr int HN = kHoist ? C::FN : 1;
+  f16x4 bvs[HN][4], gvs[EPI == kLayerNorm ? HN : 1][4], evs[EPI == kLayerNorm ? HN : 1][4];
+  auto load_cols = [&](int fn, int h) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
+      bvs[h][j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
+      if constexpr (EPI == kLayerNorm) {
+        gvs[h][j] = *reinterpret_cast<const f16x4*>(gamma + nl);
+        evs[h][j] = *reinterpret_cast<const f16x4*>(beta + nl);
+      }
+    }
+  };
+  if constexpr (kHoist) {
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
+  }
+
   if constexpr (EPI == kLayerNorm) {
     static_assert(C::BN == kHidden, "LayerNorm tile owns whole 384-wide rows");
     // v = acc + bias + residual, then two-pass row statistics: per-lane sums,
     // lane ^ 32 holds the other half of the wave's columns, LDS across wn.
+    // The residual rows arrive through the (still free) output staging area:
+    // coalesced 16-byte loads, then each lane reads its 4-column runs from
+    // LDS.  Tiles staged in passes read their runs from global memory.
+    constexpr bool kStageRes = C::NPASS == 1;
+    if constexpr (kStageRes) {
+      constexpr int CPR = kHidden / 8, PER = (C::BM * CPR + C::THREADS - 1) / C::THREADS;
 #pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
-      const int mg = min(m0 + wm * C::TM + fm * 32 + r32, M - 1);
+      for (int q = 0; q < PER; ++q) {
+        const int idx = threadIdx.x + q * C::THREADS;
+        const int r = idx / CPR, c = idx % CPR;
+        if (idx < C::BM * CPR)
+          *reinterpret_cast<f16x8*>(tile + r * C::OUT_LD + c * 8) = *reinterpret_cast<const f16x8*>(
+              residual + (size_t)min(m0 + r, M - 1) * kHidden + c * 8);
+      }
+      lds_barrier();
+    }
 #pragma unroll
-      for (int fn = 0; fn < C::FN; ++fn)
+    for (int fn = 0; fn < C::FN; ++fn) {
+      if constexpr (!kHoist) load_cols(fn, 0);
+      const int h = kHoist ? fn : 0;
+#pragma unroll
+      for (int fm = 0; fm < C::FM; ++fm) {
+        const int ml = wm * C::TM + fm * 32 + r32;
+        const int mg = min(m0 + ml, M - 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int n = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
-          const f16x4 bv = *reinterpret_cast<const f16x4*>(bias + n);
-          const f16x4 rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * kHidden + n);
+          const f16x4 rv =
+              kStageRes ? *reinterpret_cast<const f16x4*>(tile + ml * C::OUT_LD + n)
+                        : *reinterpret_cast<const f16x4*>(residual + (size_t)mg * kHidden + n);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[fm][fn][4 * j + i] += (float)bv[i] + (float)rv[i];
+          for (int i = 0; i < 4; ++i) acc[fm][fn][4 * j + i] += (float)bvs[h][j][i] + (float)rv[i];
         }
+      }
     }
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
@@ -366,7 +433,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       s += __shfl_xor(s, 32, kWave);
       if (kh == 0) red[wn * C::BM + wm * C::TM + fm * 32 + r32] = s;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
       const int row = wm * C::TM + fm * 32 + r32;
@@ -385,7 +452,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       q += __shfl_xor(q, 32, kWave);
       if (kh == 0) red[(C::WN + wn) * C::BM + row] = q;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
       const int row = wm * C::TM + fm * 32 + r32;
@@ -397,37 +464,33 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   }
 
   // fp16 tile into LDS (row pass p holds tile rows [p*PR, (p+1)*PR)), then
-  // coalesced stores.  One 32x32 block at a time; the scheduling fence keeps
-  // a single block's values live.
+  // coalesced stores, which add the residual for kResidual (16-byte loads laid
+  // out like the output rows).  One 32x32 block at a time; the scheduling
+  // fence keeps a single block's values live.
 #pragma unroll
   for (int p = 0; p < C::NPASS; ++p) {
     if (C::NPASS == 1 || wm == p) {
 #pragma unroll
-      for (int fm = 0; fm < C::FM; ++fm) {
-        const int ml = wm * C::TM + fm * 32 + r32;  // row inside the tile
-        const int mg = min(m0 + ml, M - 1);
+      for (int fn = 0; fn < C::FN; ++fn) {
+        if constexpr (!kHoist) load_cols(fn, 0);
+        const int h = kHoist ? fn : 0;
 #pragma unroll
-        for (int fn = 0; fn < C::FN; ++fn) {
+        for (int fm = 0; fm < C::FM; ++fm) {
+          const int ml = wm * C::TM + fm * 32 + r32;  // row inside the tile
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
             f16x4 o;
             if constexpr (EPI == kLayerNorm) {
-              const f16x4 gv = *reinterpret_cast<const f16x4*>(gamma + nl);
-              const f16x4 bv = *reinterpret_cast<const f16x4*>(beta + nl);
 #pragma unroll
               for (int i = 0; i < 4; ++i)
-                o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] * (float)gv[i] +
-                             (float)bv[i]);
+                o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] *
+                                 (float)gvs[h][j][i] +
+                             (float)evs[h][j][i]);
             } else {
-              const f16x4 bv =
-                  bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
-              f16x4 rv = {0, 0, 0, 0};
-              if (EPI == kResidual)
-                rv = *reinterpret_cast<const f16x4*>(residual + (size_t)mg * N + n0 + nl);
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
-                float v = acc[fm][fn][4 * j + i] + (float)bv[i] + (float)rv[i];
+                float v = acc[fm][fn][4 * j + i] + (float)bvs[h][j][i];
                 if (EPI == kGelu) v = gelu_as(v);
                 o[i] = (f16)v;
               }
@@ -438,9 +501,9 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
         }
       }
     }
-    __syncthreads();
-    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0);
-    if (p + 1 < C::NPASS) __syncthreads();
+    lds_barrier();
+    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr);
+    if (p + 1 < C::NPASS) lds_barrier();
   }
 }
 
@@ -590,16 +653,22 @@ const char* const kTileName[] = {BBH_TILES(BBH_NAME)};
 int pick_plain(int M, int N, int K) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
-  if (M <= 4096)
-    id = (qkv && M > 2048) ? 16 : 26;
+  if (M <= 2048)
+    id = (qkv || ffn1) ? 0 : 26;
+  else if (M <= 4096)
+    id = qkv ? 15 : (ffn1 || wide_k) ? 26 : 0;
+  else if (M <= 8192)
+    id = qkv ? 19 : ffn1 ? 23 : wide_k ? 26 : 0;
   else if (M <= 12288)
-    id = qkv ? 18 : ffn1 ? 26 : 0;
-  else if (M <= 24576)
-    id = qkv ? 22 : ffn1 ? 15 : wide_k ? 15 : 26;
-  else if (M < 98304)
-    id = qkv ? 19 : ffn1 ? 23 : wide_k ? 19 : 22;
+    id = qkv ? 20 : ffn1 ? 22 : wide_k ? 15 : 26;
+  else if (M <= 16384)
+    id = qkv ? 22 : ffn1 ? 15 : wide_k ? 25 : 15;
+  else if (M <= 32768)
+    id = (qkv || ffn1) ? 15 : 19;
+  else if (M <= 49152)
+    id = (qkv || ffn1) ? 15 : 17;
   else
-    id = qkv ? 18 : ffn1 ? 23 : wide_k ? 17 : 19;
+    id = qkv ? 17 : ffn1 ? 22 : 17;
   return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
 }
 
@@ -614,8 +683,10 @@ int gemm_tile(int M, int N, int K) { return gemm_mfma_ok(N, K) ? pick_plain(M, N
 // workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
 // (in place over y) and the row LayerNorm follows as its own pass.
 int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
-  *fused_ln = M > 24576;
-  return *fused_ln ? 18 : pick_plain(M, kHidden, K);
+  *fused_ln = M > 8192;
+  if (!*fused_ln) return pick_plain(M, kHidden, K);
+  if (M <= 16384) return 14;
+  return K >= 1024 ? 18 : 28;
 }
 
 const char* gemm_tile_name(int tile) {

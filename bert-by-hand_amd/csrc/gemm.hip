@@ -70,6 +70,16 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// fp32 -> fp16 of a value first rounded to fp32, as the reference's
+// __float2half(v) does.  The empty asm pins v in a VGPR: otherwise the
+// compiler may fuse the last add or fma with the conversion (v_fma_mix*_f16,
+// one rounding of the exact result) in some tile instantiations and not in
+// others, so the same row could differ by an ulp between tile shapes.
+__device__ __forceinline__ f16 to_half(float v) {
+  asm volatile("" : "+v"(v));
+  return (f16)v;
+}
+
 enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
 constexpr size_t kLdsMax = 160 * 1024;
@@ -484,15 +494,15 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
             if constexpr (EPI == kLayerNorm) {
 #pragma unroll
               for (int i = 0; i < 4; ++i)
-                o[i] = (f16)((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] *
-                                 (float)gvs[h][j][i] +
-                             (float)evs[h][j][i]);
+                o[i] = to_half((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] *
+                                   (float)gvs[h][j][i] +
+                               (float)evs[h][j][i]);
             } else {
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 float v = acc[fm][fn][4 * j + i] + (float)bvs[h][j][i];
                 if (EPI == kGelu) v = gelu_as(v);
-                o[i] = (f16)v;
+                o[i] = to_half(v);
               }
             }
             *reinterpret_cast<f16x4*>(tile + (ml - p * PR) * C::OUT_LD + nl) = o;
@@ -588,8 +598,10 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 //   27  128x192   64x96      PD 3   80 KB
 //   28  128x384   64x96 (8w) PD 2  128 KB   (owns whole rows)
 //   29  256x128   128x64     PD 3   96 KB
+//   30  128x128   64x32 (8w) PD 2   64 KB
+//   31  128x128   32x64 (8w) PD 2   64 KB
+//   32  128x192   32x96 (8w) PD 2   80 KB
 // Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD,SW>, epilogue>.
-// The table itself: X(id, BM, BN, WM, WN, SA, PD), ids dense from 0.
 // The table itself: X(id, BM, BN, WM, WN, SA, PD, SW), ids dense from 0.
 #define BBH_TILES(X) \
   X(0, 64, 64, 2, 2, 4, 0, 2) \
@@ -621,7 +633,10 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
   X(26, 64, 64, 2, 2, 2, 4, 2) \
   X(27, 128, 192, 2, 2, 2, 3, 2) \
   X(28, 128, 384, 2, 4, 2, 2, 2) \
-  X(29, 256, 128, 2, 2, 2, 3, 2)
+  X(29, 256, 128, 2, 2, 2, 3, 2) \
+  X(30, 128, 128, 2, 4, 2, 2, 2) \
+  X(31, 128, 128, 4, 2, 2, 2, 2) \
+  X(32, 128, 192, 4, 2, 2, 2, 2)
 
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
@@ -656,19 +671,17 @@ int pick_plain(int M, int N, int K) {
   if (M <= 2048)
     id = (qkv || ffn1) ? 0 : 26;
   else if (M <= 4096)
-    id = qkv ? 15 : (ffn1 || wide_k) ? 26 : 0;
+    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 31 : 30;
   else if (M <= 8192)
-    id = qkv ? 19 : ffn1 ? 23 : wide_k ? 26 : 0;
-  else if (M <= 12288)
-    id = qkv ? 20 : ffn1 ? 22 : wide_k ? 15 : 26;
+    id = qkv ? 31 : ffn1 ? 22 : wide_k ? 30 : 31;
   else if (M <= 16384)
-    id = qkv ? 22 : ffn1 ? 15 : wide_k ? 25 : 15;
+    id = qkv ? 30 : ffn1 ? 22 : 32;
   else if (M <= 32768)
-    id = (qkv || ffn1) ? 15 : 19;
-  else if (M <= 49152)
-    id = (qkv || ffn1) ? 15 : 17;
+    id = 30;
+  else if (M <= 98304)
+    id = qkv ? 31 : ffn1 ? 23 : wide_k ? 17 : 30;
   else
-    id = qkv ? 17 : ffn1 ? 22 : 17;
+    id = qkv ? 17 : ffn1 ? 31 : wide_k ? 17 : 30;
   return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
 }
 
@@ -685,8 +698,7 @@ int gemm_tile(int M, int N, int K) { return gemm_mfma_ok(N, K) ? pick_plain(M, N
 int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
   *fused_ln = M > 8192;
   if (!*fused_ln) return pick_plain(M, kHidden, K);
-  if (M <= 16384) return 14;
-  return K >= 1024 ? 18 : 28;
+  return M <= 16384 ? 14 : 28;
 }
 
 const char* gemm_tile_name(int tile) {

@@ -28,9 +28,11 @@ GEMM_SHAPES = [
     (16, 1152, 384, False), (48, 384, 384, False), (1040, 1536, 384, True),
     (1024, 384, 1536, False), (3072, 1152, 384, False), (8192, 1536, 384, True),
     (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
-    # large-M tiles (cfg5 runs M = 131072 end to end)
+    # large-M tiles (cfg5 runs M = 131072 end to end), one shape per tile bucket
+    (12288, 1152, 384, False), (16384, 384, 1536, False),
     (32768, 1152, 384, False), (32768, 1536, 384, True), (32768, 384, 384, False),
     (32768, 384, 1536, False),
+    (40000, 1152, 384, False), (40000, 1536, 384, True), (40000, 384, 1536, False),
 ]
 
 
@@ -67,7 +69,7 @@ def test_linear_reference_kat(torch_cuda, kats, tag):
 
 
 @pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384),
-                                 (32768, 384), (32768, 1536)])
+                                 (12288, 384), (16384, 1536), (32768, 384), (32768, 1536)])
 def test_linear_residual_layernorm(torch_cuda, M, K):
     torch = torch_cuda
     from bbh import engine

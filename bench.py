@@ -297,7 +297,9 @@ def main():
     else:
         epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else
                                     "2 (bias+residual), then ln384_kernel")
-        kname = f"gemm_kernel<{engine.gemm_tile_name(tile)}, {epi}>"
+        tname = engine.gemm_tile_name(tile)
+        kname = (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
+                 f"gemm_kernel<{tname}, {epi}>")
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
     if os.path.exists(tfile):

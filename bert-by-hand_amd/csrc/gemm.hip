@@ -331,7 +331,8 @@ __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ ou
   constexpr int PER = (ROWS * CPR + C::THREADS - 1) / C::THREADS;
   // Unrolled so the residual loads of several rows are in flight together
   // (by 4 when the tile is staged in passes and other accumulators are live).
-#pragma unroll(C::NPASS == 1 ? PER : 4)
+  constexpr int kUnroll = C::NPASS == 1 ? PER : 4;
+#pragma unroll kUnroll
   for (int q = 0; q < PER; ++q) {
     const int idx = threadIdx.x + q * C::THREADS;
     const int r = idx / CPR, c = idx % CPR;
@@ -517,6 +518,140 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   }
 }
 
+// ---- Weight-resident kernel for K = 384 -----------------------------------
+// The QKV and FFN1 Linears have K = 384, so one wavefront can hold the fp16 W
+// fragments of 32 output columns for the whole K in 96 VGPRs.  A workgroup of
+// 12 wavefronts (768 threads, 3 per SIMD) then owns 384 columns and walks
+// 32-row M-tiles persistently.  Only A streams through LDS: a ring of
+// wres::RING tiles of 32 x 384 (24 KB each, the 64-wide slice layout above),
+// filled with global_load_lds, two 1 KB copies per wavefront per tile.  No W
+// moves after the prologue, and each 32x32x16 MFMA reads one 1 KB A fragment
+// from LDS.  Bytes moved from L2 per FLOP drop ~6x against a 128x128 tile;
+// on MI355X that delivery, not the matrix cores, bounds the tiled kernels.
+//
+// The k order, operand layout, epilogue arithmetic and fp16 rounding are
+// those of the tiled kernels, so every output is bit-identical whichever
+// kernel computes it.
+namespace wres {
+constexpr int NW = 12, THREADS = 64 * NW, K = 384, KS = K / 16, BM = 32, RING = 4;
+constexpr int TILE = BM * K;                   // halves per A tile
+constexpr int CPW = (BM * K * 2 / 1024) / NW;  // 1 KB copies per wavefront per tile
+constexpr int COLS = NW * 32;                  // output columns per workgroup
+constexpr size_t LDS = (size_t)RING * TILE * sizeof(f16);
+static_assert((BM * K * 2 / 1024) % NW == 0, "copies per wavefront");
+}  // namespace wres
+
+template <int EPI>
+__global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __restrict__ A,
+                                                                  const f16* __restrict__ W,
+                                                                  const f16* __restrict__ bias,
+                                                                  f16* __restrict__ out, int M,
+                                                                  int N) {
+  using namespace wres;
+  HIP_DYNAMIC_SHARED(f16, smem);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r32 = lane & 31, kh = lane >> 5;
+  // Workgroup b runs on XCD b % 8.  The nb column blocks of one M-group are
+  // placed on the same XCD, so each A tile comes from HBM once per XCD.
+  const int nb = N / COLS, x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int ng = slot % nb, mg = (slot / nb) * 8 + x, groups = (int)(gridDim.x >> 3) / nb * 8;
+  const int n0 = ng * COLS + wave * 32;
+  // W fragment of k-step s: row n0 + r32, k = 16 s + 8 kh .. +7 (the tiled
+  // kernels' k mapping).
+  f16x8 w[KS];
+#pragma unroll
+  for (int st = 0; st < KS; ++st)
+    w[st] = *reinterpret_cast<const f16x8*>(W + (size_t)(n0 + r32) * K + 16 * st + 8 * kh);
+  f16x4 bq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    bq[j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + 8 * j + 4 * kh) : f16x4{0, 0, 0, 0};
+  const int ntiles = (M + BM - 1) / BM;
+  const int my = mg < ntiles ? (ntiles - 1 - mg) / groups + 1 : 0;
+  // Copy g of a tile: slice g / 4, rows (g % 4) * 8 .. +7 (copy_group's lane
+  // layout); rows past M read row M - 1.
+  auto issue = [&](int i) {
+    const int t = mg + i * groups;
+    f16* dst = smem + (i % RING) * TILE;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int g = wave * CPW + j, sl = g >> 2, r = (g & 3) * 8 + (lane >> 3);
+      const int cl = (lane & 7) ^ Slice<64>::f(r);
+      __builtin_amdgcn_global_load_lds(
+          A + (size_t)min(t * BM + r, M - 1) * K + sl * 64 + cl * 8,
+          (__attribute__((address_space(3))) void*)(dst + sl * 2048 + (g & 3) * 512), 16, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < RING - 1; ++i)
+    if (i < my) issue(i);
+  for (int i = 0; i < my; ++i) {
+    // Tile i has landed once at most the copies of tiles i+1 .. i+RING-2 are
+    // outstanding (copies retire in issue order; the epilogue stores counted
+    // in vmcnt only make the wait stricter).
+    if (i + RING - 2 < my)
+      wait_vm<CPW * (RING - 2)>();
+    else
+      wait_vm<0>();
+    lds_barrier();  // tile i visible to all; tile i-1's slot free
+    if (i + RING - 1 < my) issue(i + RING - 1);
+    const f16* tA = smem + (i % RING) * TILE;
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    f16x8 a[2];
+    a[0] = *reinterpret_cast<const f16x8*>(tA + Slice<64>::off(r32, kh));
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      if (st + 1 < KS) {
+        const int s1 = st + 1;
+        a[s1 & 1] = *reinterpret_cast<const f16x8*>(tA + (s1 >> 2) * 2048 +
+                                                     Slice<64>::off(r32, 2 * (s1 & 3) + kh));
+      }
+      acc = mfma32(w[st], a[st & 1], acc);
+    }
+    // acc[i] = D(n0 + 8 (i / 4) + 4 kh + i % 4, m): four 4-column runs of row m.
+    const int m = (mg + i * groups) * BM + r32;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[4 * j + e] + (float)bq[j][e];
+        if (EPI == kGelu) v = gelu_as(v);
+        o[e] = to_half(v);
+      }
+      if (m < M) *reinterpret_cast<f16x4*>(out + (size_t)m * N + n0 + 8 * j + 4 * kh) = o;
+    }
+  }
+}
+
+// The weight-resident kernel serves K = 384 and N a multiple of 384, from
+// the M where sweeps on MI355X show it ahead of the tiled kernels: 24576 for
+// FFN1 (N = 1536, where it saves the most L2 traffic per row), 49152 for QKV.
+bool wres_ok(int M, int N, int K) {
+  return K == wres::K && N % wres::COLS == 0 && M >= (N >= 1536 ? 24576 : 49152);
+}
+
+template <int EPI>
+hipError_t launch_wres(const f16* A, const f16* W, const f16* bias, f16* out, int M, int N,
+                       hipStream_t s) {
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_wres_kernel<EPI>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wres::LDS);
+  if (attr != hipSuccess) return attr;
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  // One workgroup per CU: 8 XCDs x nb column blocks x q M-groups per XCD.
+  const int nb = N / wres::COLS, ntiles = (M + wres::BM - 1) / wres::BM;
+  const int q = max(1, min(cus / (8 * nb), (ntiles + 7) / 8));
+  hipLaunchKernelGGL((gemm_wres_kernel<EPI>), dim3(8 * nb * q), dim3(wres::THREADS), wres::LDS, s,
+                     A, W, bias, out, M, N);
+  return hipGetLastError();
+}
+
 // Any-shape fallback (the role of src/kernels/matmul.cu:34-59): 16x16 output
 // tile per 256 threads, fp32 accumulate, operands staged through LDS.
 __global__ __launch_bounds__(256) void gemm_generic_kernel(
@@ -689,7 +824,10 @@ int pick_plain(int M, int N, int K) {
 
 bool gemm_mfma_ok(int N, int K) { return N % 64 == 0 && K % 64 == 0; }
 
-int gemm_tile(int M, int N, int K) { return gemm_mfma_ok(N, K) ? pick_plain(M, N, K) : -1; }
+int gemm_tile(int M, int N, int K) {
+  if (!gemm_mfma_ok(N, K)) return -1;
+  return wres_ok(M, N, K) ? kTiles : pick_plain(M, N, K);
+}
 
 // Large M: one kernel whose 128x384 tile owns whole rows.  Smaller M: a tile
 // that owns whole rows leaves most CUs idle and streams all of W per
@@ -702,6 +840,7 @@ int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
 }
 
 const char* gemm_tile_name(int tile) {
+  if (tile == kTiles) return "WRes<12x32,384>";
   return (tile >= 0 && tile < kTiles) ? kTileName[tile] : "generic";
 }
 
@@ -716,6 +855,8 @@ hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int 
                        gelu ? 1 : 0);
     return hipGetLastError();
   }
+  if (wres_ok(M, N, K))
+    return gelu ? launch_wres<kGelu>(A, W, bias, C, M, N, s) : launch_wres<kBias>(A, W, bias, C, M, N, s);
   const int id = pick_plain(M, N, K);
   return gelu ? launch_id<kGelu>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s)
               : launch_id<kBias>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s);
@@ -748,6 +889,10 @@ extern "C" int bbh_tune_gemm(int id, int epi, const void* A, const void* W, cons
   auto be = static_cast<const f16*>(beta);
   auto o = static_cast<f16*>(out);
   auto st = static_cast<hipStream_t>(stream);
+  if (id == kTiles) {  // the weight-resident kernel, any M
+    if (K != wres::K || N % wres::COLS != 0 || epi > 1) return hipErrorInvalidValue;
+    return epi ? launch_wres<kGelu>(a, w, b, o, M, N, st) : launch_wres<kBias>(a, w, b, o, M, N, st);
+  }
   switch (epi) {
     case 0: return launch_id<kBias>(id, a, w, b, r, g, be, o, M, N, K, eps, st);
     case 1: return launch_id<kGelu>(id, a, w, b, r, g, be, o, M, N, K, eps, st);

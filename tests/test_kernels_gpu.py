@@ -33,6 +33,8 @@ GEMM_SHAPES = [
     (32768, 1152, 384, False), (32768, 1536, 384, True), (32768, 384, 384, False),
     (32768, 384, 1536, False),
     (40000, 1152, 384, False), (40000, 1536, 384, True), (40000, 384, 1536, False),
+    # the weight-resident K = 384 kernel (QKV from M = 49152, FFN1 from 24576), ragged last tile
+    (50000, 1152, 384, False),
 ]
 
 
@@ -50,6 +52,27 @@ def test_linear(torch_cuda, M, N, K, gelu):
     got = _np(C)
     assert np.abs(got - want).max() <= TOL
     assert cosine_rows(got.ravel(), want.ravel()) >= 0.9999
+
+
+@pytest.mark.parametrize("N,gelu", [(1152, False), (1536, True), (384, False)])
+def test_linear_rows_identical_across_kernels(torch_cuda, N, gelu):
+    # The first rows of a large-M GEMM equal the same rows computed alone:
+    # every kernel accumulates in the same k order and rounds the same way.
+    # M = 50000 runs QKV and FFN1 on the weight-resident kernel and N = 384 on
+    # a 128x128 tile; M = 2048 runs all three on 64x64 tiles.
+    torch = torch_cuda
+    from bbh import engine
+
+    M, K, m = 50000, 384, 2048
+    rng = np.random.default_rng(N + 11)
+    A, W, b = _h(rng, (M, K)), _h(rng, (N, K), 1.0 / np.sqrt(K)), _h(rng, (N,), 0.1)
+    dA, dW, db = to_dev(torch, A), to_dev(torch, W), to_dev(torch, b)
+    big = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    small = torch.empty((m, N), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(dA, dW, big, M, N, K, bias=db, gelu=gelu)
+    engine.launch_matmul(dA[:m], dW, small, m, N, K, bias=db, gelu=gelu)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(big[:m]), _np(small))
 
 
 @pytest.mark.parametrize("tag", ["small", "real"])

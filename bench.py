@@ -287,25 +287,30 @@ def main():
     per_op = {}
     for (op, tile, fused), c in classes.items():
         per_op[op] = per_op.get(op, 0.0) + c["ms"] / args.steps
+
+    def kernel_name(op, tile, fused):
+        if op == "attention":
+            return "attention_kernel"
+        epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else
+                                    "2 (bias+residual), then ln384_kernel")
+        tname = engine.gemm_tile_name(tile)
+        return (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
+                f"gemm_kernel<{tname}, {epi}>")
+
     key = max(classes, key=lambda k: classes[k]["ms"])
     op, tile, fused = key
     c = classes[key]
     avg_s = c["ms"] / c["n"] / 1e3
     ach = c["flops"] / c["n"] / avg_s
-    if op == "attention":
-        kname = "attention_kernel"
-    else:
-        epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else
-                                    "2 (bias+residual), then ln384_kernel")
-        tname = engine.gemm_tile_name(tile)
-        kname = (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
-                 f"gemm_kernel<{tname}, {epi}>")
+    kname = kernel_name(op, tile, fused)
+    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE summary
+    # (one entry per leading kernel class of the profiled run)
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
     if os.path.exists(tfile):
-        t = json.load(open(tfile))
-        if t.get("kernel") == kname and t.get("m") == sorted(c["m"]):
-            traffic = t["traffic_bytes_per_launch"]
+        for t in json.load(open(tfile)).get("kernels", []):
+            if t.get("kernel") == kname and t.get("op") == op and t.get("m") == sorted(c["m"]):
+                traffic = t["traffic_bytes_per_launch"]
     out["roofline"] = {
         "bound": "mfma", "achieved": round(ach / 1e12, 2), "peak": PEAK_FP16_DENSE / 1e12,
         "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_DENSE, 4), "traffic": traffic,
@@ -316,8 +321,24 @@ def main():
         "algorithmic_bytes_per_launch": round(c["bytes"] / c["n"]),
         "share_of_op_time": round(c["ms"] / sum(v["ms"] for v in classes.values()), 3)}
     out["op_ms_per_step"] = {k: round(v, 4) for k, v in sorted(per_op.items())}
+
+    top = sorted(classes, key=lambda k: -classes[k]["ms"])[:3]
+    out["top_kernel_classes"] = [
+        {"kernel": kernel_name(*k), "op": k[0], "m": sorted(classes[k]["m"]),
+         "avg_launch_us": round(classes[k]["ms"] / classes[k]["n"] * 1e3, 2),
+         "algorithmic_bytes_per_launch": round(classes[k]["bytes"] / classes[k]["n"]),
+         "share_of_op_time": round(classes[k]["ms"] / sum(v["ms"] for v in classes.values()), 3)}
+        for k in top]
+    by_m = {}
+    for r in recs:
+        d = by_m.setdefault(r["op"], {}).setdefault(r["m"], [0.0, 0])
+        d[0] += r["ms"]
+        d[1] += 1
+    out["op_us_per_launch_by_m"] = {op: {m: round(t / n * 1e3, 2) for m, (t, n) in sorted(d.items())}
+                                    for op, d in sorted(by_m.items())}
     log("roofline", out["roofline"])
     log("op ms per step", out["op_ms_per_step"])
+    log("op us per launch by M", out["op_us_per_launch_by_m"])
 
     buf = gemm_buffers(torch, 131072)
     if not args.no_extras:

@@ -796,25 +796,29 @@ constexpr int kTiles = sizeof(kBnOf) / sizeof(kBnOf[0]);
 const char* const kTileName[] = {BBH_TILES(BBH_NAME)};
 #undef BBH_NAME
 
-// Tile config per shape, from sweeps on MI355X over the encoder's four
-// shapes (N, K) = (1152, 384) QKV, (1536, 384) FFN1, (384, 384) O-proj and
-// (384, 1536) FFN2.  Small M wants many small tiles (latency, CU coverage);
-// large M wants big tiles (L2 and LDS traffic per MFMA).
+// Tile config per shape, from interleaved A/B timings (medians of several
+// rounds) on MI355X over the encoder's four shapes (N, K) = (1152, 384) QKV,
+// (1536, 384) FFN1, (384, 384) O-proj and (384, 1536) FFN2.  QKV and FFN1 at
+// large M run on the weight-resident kernel instead (wres_ok).  Small M wants
+// many small tiles (latency, CU coverage); large M wants big tiles (L2 and
+// LDS traffic per MFMA).
 int pick_plain(int M, int N, int K) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
   if (M <= 2048)
-    id = (qkv || ffn1) ? 0 : 26;
+    id = qkv ? 30 : ffn1 ? 0 : 26;
+  else if (M <= 3072)
+    id = qkv ? 30 : ffn1 ? 26 : wide_k ? 26 : 0;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 31 : 30;
+    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 26 : 0;
+  else if (M <= 6144)
+    id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)
-    id = qkv ? 31 : ffn1 ? 22 : wide_k ? 30 : 31;
+    id = wide_k ? 31 : 30;
   else if (M <= 16384)
-    id = qkv ? 30 : ffn1 ? 22 : 32;
-  else if (M <= 32768)
-    id = 30;
-  else if (M <= 98304)
-    id = qkv ? 31 : ffn1 ? 23 : wide_k ? 17 : 30;
+    id = wide_k ? 32 : 30;
+  else if (M <= 49152)
+    id = wide_k ? 19 : 30;
   else
     id = qkv ? 17 : ffn1 ? 31 : wide_k ? 17 : 30;
   return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
@@ -836,7 +840,7 @@ int gemm_tile(int M, int N, int K) {
 int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
   *fused_ln = M > 8192;
   if (!*fused_ln) return pick_plain(M, kHidden, K);
-  return M <= 16384 ? 14 : 28;
+  return M <= 16384 ? 14 : K >= 1024 ? 18 : 28;
 }
 
 const char* gemm_tile_name(int tile) {

@@ -272,20 +272,34 @@ bbh_status timed_op(OpTimer* t, hipStream_t s, const bbh_launch_time& meta, F&& 
   return st;
 }
 
+// A run of sentences with one padded length inside a forward: its masks, its
+// shape, and its first row in the workspace's hidden buffers.  One forward
+// may hold several segments: every Linear works per token, so the GEMMs run
+// once over all rows and only attention, the embedding's positions and the
+// pooling look at segment boundaries.
+struct Segment {
+  const int32_t* mask;
+  int batch, seq;
+  size_t row;
+};
+
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                               const int32_t* mask, f16* out, int batch, int seq, hipStream_t s,
+                               const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
                                OpTimer* t = nullptr) {
-  const int M = batch * seq, H = BBH_HIDDEN;
+  const int H = BBH_HIDDEN;
   BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H), 0, M, 3 * H, H, 0.f}, [&] {
     return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
                                   bbh::Act::kNone, s),
                         "qkv gemm");
   }));
-  BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, batch, seq, BBH_NUM_HEADS, 0.f}, [&] {
-    return check_launch(bbh::attention(ws->qkv, mask, ws->ctx, batch, BBH_NUM_HEADS, seq,
-                                       kScale, s),
-                        "attention");
-  }));
+  for (int g = 0; g < n_segs; ++g) {
+    const Segment& sg = segs[g];
+    BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, sg.batch, sg.seq, BBH_NUM_HEADS, 0.f}, [&] {
+      return check_launch(bbh::attention(ws->qkv + sg.row * 3 * H, sg.mask, ws->ctx + sg.row * H,
+                                         sg.batch, BBH_NUM_HEADS, sg.seq, kScale, s),
+                          "attention");
+    }));
+  }
   bool fused;
   const int tile = bbh::gemm_residual_ln_tile(M, H, &fused);
   return timed_op(t, s, {BBH_OP_O_PROJ_LN, tile, fused ? 1 : 0, M, H, H, 0.f}, [&] {
@@ -295,9 +309,16 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
   });
 }
 
-bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                         f16* out, int batch, int seq, hipStream_t s, OpTimer* t = nullptr) {
-  const int M = batch * seq, H = BBH_HIDDEN, F = BBH_FFN_DIM;
+bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                               const int32_t* mask, f16* out, int batch, int seq, hipStream_t s,
+                               OpTimer* t = nullptr) {
+  const Segment one{mask, batch, seq, 0};
+  return run_attention_block(ws, L, hidden, &one, 1, out, batch * seq, s, t);
+}
+
+bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                        f16* out, int M, hipStream_t s, OpTimer* t = nullptr) {
+  const int H = BBH_HIDDEN, F = BBH_FFN_DIM;
   BBH_TRY(timed_op(t, s, {BBH_OP_FFN1_GELU, bbh::gemm_tile(M, F, H), 0, M, F, H, 0.f}, [&] {
     return check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, F, H, bbh::Act::kGelu, s),
                         "ffn1 gemm");
@@ -311,23 +332,43 @@ bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16
   });
 }
 
-// Embeddings + 6 layers; the last layer writes `final_out` (which may be
-// ws->attn_out: the FFN2+LN epilogue reads each residual element before the
-// same thread overwrites it).
-bbh_status run_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
-                      const int32_t* types, const int32_t* mask, f16* final_out, int batch,
-                      int seq, hipStream_t s, OpTimer* t = nullptr) {
-  BBH_TRY(check_launch(bbh::embedding_ln(ids, types, m->word, m->pos, m->type, m->emb_g,
-                                         m->emb_b, ws->ping, batch, seq, BBH_LAYER_NORM_EPS, s),
-                       "embedding+ln"));
+bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                         f16* out, int batch, int seq, hipStream_t s, OpTimer* t = nullptr) {
+  return run_ffn_rows(ws, L, hidden, out, batch * seq, s, t);
+}
+
+// Embeddings + 6 layers over the segments' rows; the last layer writes
+// `final_out` (which may be ws->attn_out: the FFN2+LN epilogue reads each
+// residual element before the same thread overwrites it).  Segment g's
+// tokens are at ids + tok[g] (types and masks likewise).
+bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                           const int32_t* types, const int64_t* tok, const Segment* segs,
+                           int n_segs, f16* final_out, hipStream_t s, OpTimer* t = nullptr) {
+  int M = 0;
+  for (int g = 0; g < n_segs; ++g) {
+    const Segment& sg = segs[g];
+    BBH_TRY(check_launch(bbh::embedding_ln(ids + tok[g], types + tok[g], m->word, m->pos, m->type,
+                                           m->emb_g, m->emb_b, ws->ping + sg.row * BBH_HIDDEN,
+                                           sg.batch, sg.seq, BBH_LAYER_NORM_EPS, s),
+                         "embedding+ln"));
+    M += sg.batch * sg.seq;
+  }
   f16* cur = ws->ping;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
-    BBH_TRY(run_attention_block(ws, m->layers[i], cur, mask, ws->attn_out, batch, seq, s, t));
-    BBH_TRY(run_ffn_block(ws, m->layers[i], ws->attn_out, nxt, batch, seq, s, t));
+    BBH_TRY(run_attention_block(ws, m->layers[i], cur, segs, n_segs, ws->attn_out, M, s, t));
+    BBH_TRY(run_ffn_rows(ws, m->layers[i], ws->attn_out, nxt, M, s, t));
     cur = nxt;
   }
   return BBH_OK;
+}
+
+bbh_status run_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                      const int32_t* types, const int32_t* mask, f16* final_out, int batch,
+                      int seq, hipStream_t s, OpTimer* t = nullptr) {
+  const Segment one{mask, batch, seq, 0};
+  const int64_t tok0 = 0;
+  return run_encode_segs(ws, m, ids, types, &tok0, &one, 1, final_out, s, t);
 }
 
 }  // namespace
@@ -859,9 +900,11 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
   }
   if (n_batches == 0) return BBH_OK;
   // Runs of consecutive batches with one seq that sit back to back in the
-  // token arrays and in emb are one (sum of batches, seq) forward, up to a
-  // workspace's rows: sentences are independent, so each keeps exactly the
-  // embedding it gets alone, while the kernels see a larger M.
+  // token arrays and in emb are one (sum of batches, seq) segment: sentences
+  // are independent, so each keeps the embedding it gets alone while the
+  // kernels see a larger M.  (Bit for bit where the LayerNorm path stays the
+  // same; a larger M can move it into the GEMM epilogue, whose row
+  // statistics sum in another order.)
   struct Run {
     int first, batch;
   };
@@ -883,35 +926,81 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     }
     runs.push_back({i, batch_sizes[i]});
   }
-  // Largest run first onto the least-loaded stream (longest-processing-time
-  // order), so the streams finish together.
+  // Runs are packed into groups, one forward each, up to a workspace's rows:
+  // the GEMMs run over all rows of a group and only attention, the
+  // embedding's positions and the pooling work per run.  Largest run first,
+  // into a new group while there are fewer groups than streams, else into
+  // the group with the fewest rows that still has room (a new one if none
+  // has).  Groups then go largest first to the least-loaded stream.
   const int n_runs = (int)runs.size();
-  std::vector<int> order(n_runs);
-  for (int r = 0; r < n_runs; ++r) order[r] = r;
   auto rows_of = [&](int r) { return (size_t)runs[r].batch * seqs[runs[r].first]; };
-  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return rows_of(a) > rows_of(b); });
+  std::vector<int> by_size(n_runs);
+  for (int r = 0; r < n_runs; ++r) by_size[r] = r;
+  std::stable_sort(by_size.begin(), by_size.end(),
+                   [&](int a, int b) { return rows_of(a) > rows_of(b); });
+  struct Group {
+    std::vector<int> runs;
+    size_t rows = 0;
+  };
+  std::vector<Group> groups;
+  for (int r : by_size) {
+    int best = -1;
+    if ((int)groups.size() >= n) {
+      for (int g = 0; g < (int)groups.size(); ++g)
+        if (groups[g].rows + rows_of(r) <= cap && (best < 0 || groups[g].rows < groups[best].rows))
+          best = g;
+    }
+    if (best < 0) {
+      groups.push_back({});
+      best = (int)groups.size() - 1;
+    }
+    groups[best].runs.push_back(r);
+    groups[best].rows += rows_of(r);
+  }
+  const int n_groups = (int)groups.size();
+  std::vector<int> order(n_groups);
+  for (int g = 0; g < n_groups; ++g) {
+    order[g] = g;
+    std::sort(groups[g].runs.begin(), groups[g].runs.end());  // batch order inside a group
+  }
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int a, int b) { return groups[a].rows > groups[b].rows; });
   std::vector<size_t> load(n, 0);
-  std::vector<int> stream_of(n_runs);
-  for (int r : order) {
+  std::vector<int> stream_of(n_groups);
+  for (int g : order) {
     const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-    stream_of[r] = j;
-    load[j] += rows_of(r);
+    stream_of[g] = j;
+    load[j] += groups[g].rows;
   }
   const hipStream_t caller = S(stream);
   BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
-  const int used = n_runs < n ? n_runs : n;  // streams with work: the first `used`
+  const int used = n_groups < n ? n_groups : n;  // streams with work: the first `used`
   for (int j = 0; j < used; ++j)
     BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
-  for (int r : order) {
-    const int j = stream_of[r], i = runs[r].first, batch = runs[r].batch, seq = seqs[i];
-    const int64_t o = tok_offsets[i];
-    f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
+  std::vector<Segment> segs;
+  std::vector<int64_t> tok;
+  for (int g : order) {
+    const int j = stream_of[g];
     bbh_workspace* w = pool->ws[j];
-    BBH_TRY(run_encode(w, m, ids + o, types + o, mask + o, w->attn_out, batch, seq,
-                       pool->streams[j], pool->timer));
-    BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out, mask + o, out, batch, seq,
-                                             pool->streams[j]),
-                         "pool+normalize"));
+    segs.clear();
+    tok.clear();
+    size_t row = 0;
+    for (int r : groups[g].runs) {
+      const int i = runs[r].first;
+      segs.push_back({mask + tok_offsets[i], runs[r].batch, seqs[i], row});
+      tok.push_back(tok_offsets[i]);
+      row += rows_of(r);
+    }
+    BBH_TRY(run_encode_segs(w, m, ids, types, tok.data(), segs.data(), (int)segs.size(),
+                            w->attn_out, pool->streams[j], pool->timer));
+    for (size_t k = 0; k < segs.size(); ++k) {
+      const int i = runs[groups[g].runs[k]].first;
+      f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
+      BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out + segs[k].row * BBH_HIDDEN,
+                                               segs[k].mask, out, segs[k].batch, segs[k].seq,
+                                               pool->streams[j]),
+                           "pool+normalize"));
+    }
   }
   for (int j = 0; j < used; ++j) {
     BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");

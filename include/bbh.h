@@ -160,16 +160,22 @@ bbh_status bbh_graph_free(bbh_graph *g);
  * tok_offsets[i] of the device arrays and writes batch_sizes[i] rows of emb
  * starting at row emb_rows[i].  The size/offset arrays are HOST arrays.
  * Consecutive batches with the same seq that are adjacent both in the token
- * arrays and in emb run as one forward of their summed batch, up to a pool
- * workspace's max_batch*max_seq rows, so a caller that packs equal-seq
- * batches together gets larger kernels with every batch's padding unchanged
- * (the reference's corpus benchmark instead re-sorts sentences by length,
- * bench/corpus.cu:79-118).  Every sentence still gets the embedding it gets
- * alone, since sentences never interact.  Runs go largest first to the
- * least-loaded stream.  The call orders itself after prior
- * work on `stream` and makes later work on `stream` wait for all batches; it
- * returns without a host sync.  A pool must not be used by two overlapping
- * calls. */
+ * arrays and in emb form one run (one attention launch over their summed
+ * batch), and runs are packed into groups of up to a pool workspace's
+ * max_batch*max_seq rows: each group is one forward whose GEMMs cover all of
+ * its rows, while attention, the embedding's positions and the pooling go
+ * run by run.  A caller that packs equal-seq batches together thus gets
+ * larger kernels with every batch's padding unchanged (the reference's corpus
+ * benchmark instead re-sorts sentences by length, bench/corpus.cu:79-118).
+ * Sentences never interact, so every sentence gets the embedding it gets
+ * alone: bit for bit while its LayerNorm path is the one a lone batch takes,
+ * else to within the rounding of the LayerNorm row statistics (larger groups
+ * fuse the LayerNorm into the GEMM epilogue).  Groups are formed largest run
+ * first, one per stream while streams remain, then into the group with the
+ * fewest rows that has room; they go largest first to the least-loaded
+ * stream.  The call orders itself after prior work on `stream` and makes
+ * later work on `stream` wait for all batches; it returns without a host
+ * sync.  A pool must not be used by two overlapping calls. */
 typedef struct bbh_pool bbh_pool;
 bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
 bbh_status bbh_pool_free(bbh_pool *pool);

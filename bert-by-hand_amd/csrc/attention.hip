@@ -22,12 +22,22 @@
 // the lane, and V^T is read with one 16-byte LDS load per MFMA.
 //
 // Softmax in fp32, base 2: the 1/sqrt(32) scale (src/model/encoder.cu:28) and
-// log2(e) fold into one FMA before v_exp_f32; the row max needs one exchange
-// with lane ^ 32.  Mask semantics follow src/kernels/softmax.cu:35-62: keys
+// log2(e) fold into one FMA before v_exp_f32; the row max needs one
+// permlane32 swap (lane ^ 32).  The running max is updated lazily: the
+// accumulator is rescaled only when some row's max rises by more than 2^8 in
+// probability, so most chunks skip the 16 multiplies and the extra exp.  Row
+// sums add the fp16 probabilities (the values the P.V MFMA consumes) with
+// v_dot2_f32_f16.  Mask semantics follow src/kernels/softmax.cu:35-62: keys
 // with mask 0 are dropped and a query whose keys are all masked gets a zero
-// context.  32-key chunks are classified once per workgroup: fully masked
-// chunks are skipped (their contribution is exactly zero), fully unmasked
-// chunks need no mask arithmetic.
+// context.  A bitmap of unmasked keys per 32-key chunk, one ballot per 64
+// keys, lets fully masked chunks be skipped (their contribution is exactly
+// zero) and fully unmasked chunks run without mask arithmetic.
+//
+// Short sequences are bound by the global round trip: all of a workgroup's
+// loads (Q, K, V, mask) are issued before its single barrier, and the output
+// goes out through LDS as 16-byte stores of 64 contiguous bytes per row.
+// Long sequences are bound by exp + MFMA issue: a wavefront then takes two
+// query tiles at once, sharing each K and V^T operand read between them.
 
 #include "kernels.h"
 
@@ -46,17 +56,31 @@ __device__ __forceinline__ int ks_off(int key, int c) {
   return key * 32 + ((c ^ ((key >> 2) & 3)) << 3);
 }
 
-size_t attn_lds_bytes(int seq) {
+// Stride (halves) of a wavefront's 32 x 32 output staging tile in LDS.
+constexpr int kStageLd = 40;
+
+size_t attn_lds_bytes(int seq, int staged_waves) {
   const int seqp = (seq + 31) & ~31;
   return (size_t)seqp * 32 * 2 + (size_t)32 * (seqp + 8) * 2 + (size_t)seqp * 4 +
-         (size_t)(seqp / 32) * 4;
+         (size_t)((seqp / 32 + 3) & ~3) * 4 + (size_t)staged_waves * 32 * kStageLd * 2;
 }
 
-template <int NW>
-__global__ __launch_bounds__(64 * NW) void attention_kernel(const f16* __restrict__ qkv,
-                                                            const int32_t* __restrict__ mask,
-                                                            f16* __restrict__ out, int batch,
-                                                            int seq, int heads, float c) {
+// Largest step (log2 units) the running row max may lag the true one: while
+// every row's chunk max stays within it of the stored max, probabilities are
+// taken against the stored max (each at most 2^kLazy, exact in fp16 and fp32)
+// and the accumulator is not rescaled.
+constexpr float kLazy = 8.f;
+
+// A wavefront works on T query tiles at once (T = 1 or 2): the tiles share
+// every K and V^T operand read from LDS, and their two dependency chains
+// (scores -> max -> exp -> P.V) interleave.  The workgroup's NW wavefronts
+// take tile groups round robin.
+// F: 1 stage the output through LDS, 2 put that staging in the K/V area
+// (one tile group per wavefront).
+template <int NW, int T, int F>
+__global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
+    const f16* __restrict__ qkv, const int32_t* __restrict__ mask, f16* __restrict__ out,
+    int batch, int seq, int heads, float c) {
   HIP_DYNAMIC_SHARED(f16, smem);
   // (sequence, head) of this workgroup; all heads of a sequence go to one XCD
   // (workgroup id % 8) back to back, so its QKV rows are fetched into one L2.
@@ -64,14 +88,31 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const f16* __restric
   const int b = (k / heads) * 8 + x, h = k % heads;
   if (b >= batch) return;
   const int seqp = (seq + 31) & ~31, nch = seqp >> 5, VLD = seqp + 8;
-  f16* Ks = smem;                                          // [seqp][32]
-  f16* Vt = Ks + seqp * 32;                                // [32][VLD]
-  float* mb = reinterpret_cast<float*>(Vt + 32 * VLD);     // [seqp]: 0 or -inf
-  int* cf = reinterpret_cast<int*>(mb + seqp);             // [nch]: 0 masked, 1 open, 2 mixed
+  f16* Ks = smem;                                              // [seqp][32]
+  f16* Vt = Ks + seqp * 32;                                    // [32][VLD]
+  float* mb = reinterpret_cast<float*>(Vt + 32 * VLD);         // [seqp]: 0 or -inf
+  uint32_t* cm = reinterpret_cast<uint32_t*>(mb + seqp);       // [nch]: unmasked-key bitmaps
+  f16* stage = reinterpret_cast<f16*>(cm + ((nch + 3) & ~3));  // [NW*T][32][kStageLd]
   const int hid = heads * kHeadDim, ld = 3 * hid;
   const f16* base = qkv + (size_t)b * seq * ld + h * kHeadDim;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r32 = lane & 31, kh = lane >> 5;
   constexpr int NT = 64 * NW;
+
+  // Q of this wavefront's first tile group, issued before the K/V staging so
+  // the two global round trips overlap.  Tile t of group g is
+  // wave + NW*(T*g + t); a tile past the sequence (T = 2, odd tile count)
+  // reads clamped rows and stores nothing.
+  f16x8 q0[T], q1[T];
+  auto load_q = [&](int g) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int q = (wave + NW * (T * g + t)) * 32 + r32;
+      const f16* qrow = base + (size_t)min(q, seq - 1) * ld;
+      q0[t] = *reinterpret_cast<const f16x8*>(qrow + 8 * kh);
+      q1[t] = *reinterpret_cast<const f16x8*>(qrow + 16 + 8 * kh);
+    }
+  };
+  load_q(0);
 
   for (int i = tid; i < seqp * 4; i += NT) {  // K: 16 bytes per (key, 8 dims)
     const int key = i >> 2, ch = i & 3;
@@ -94,89 +135,196 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const f16* __restric
       *reinterpret_cast<f16x4*>(Vt + (4 * dq + e) * VLD + 4 * kq) = col;
     }
   }
-  for (int j = tid; j < seqp; j += NT)
-    mb[j] = (j < seq && mask[(size_t)b * seq + j] != 0) ? 0.f : -INFINITY;
-  __syncthreads();
-  for (int ch = tid; ch < nch; ch += NT) {
-    int on = 0;
-    for (int j = 0; j < 32; ++j) on += (mb[ch * 32 + j] == 0.f);
-    cf[ch] = on == 0 ? 0 : (on == 32 ? 1 : 2);
+  if (wave == NW - 1) {  // key bias and bitmaps of unmasked keys, 64 keys per ballot
+    const int32_t* mrow = mask + (size_t)b * seq;
+    int mv[kMaxPos / 64];
+#pragma unroll
+    for (int j = 0; j < kMaxPos / 64; ++j) {
+      const int key = 64 * j + lane;
+      mv[j] = (64 * j < seq && key < seq) ? mrow[key] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxPos / 64; ++j) {
+      if (2 * j >= nch) break;
+      if (64 * j + lane < seqp) mb[64 * j + lane] = mv[j] != 0 ? 0.f : -INFINITY;
+      const unsigned long long on = __ballot(mv[j] != 0);
+      if (lane == 0) cm[2 * j] = (uint32_t)on;
+      if (lane == 1 && 2 * j + 1 < nch) cm[2 * j + 1] = (uint32_t)(on >> 32);
+    }
   }
   __syncthreads();
 
-  const int wave = tid >> 6, lane = tid & 63, r32 = lane & 31, kh = lane >> 5;
   const int krow = key_of_row(r32);
+  const uint32_t cml = lane < nch ? cm[lane] : 0u;  // lane j holds chunk j's bitmap
+  const float lag = kLazy / c;                      // kLazy in raw-score units
   const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int qt = wave; qt < nch; qt += NW) {
-    const int q = qt * 32 + r32;
-    const f16* qrow = base + (size_t)min(q, seq - 1) * ld;
-    const f16x8 q0 = *reinterpret_cast<const f16x8*>(qrow + 8 * kh);
-    const f16x8 q1 = *reinterpret_cast<const f16x8*>(qrow + 16 + 8 * kh);
-    f32x16 o = zero;
-    float m = -INFINITY, l = 0.f;
+  const f16x2 ones = {(f16)1.f, (f16)1.f};
+  for (int g = 0; wave + NW * T * g < nch; ++g) {
+    if (g > 0) load_q(g);
+    f32x16 o[T];
+    float m[T], l[T];  // running max (raw scores) and sum of the fp16 probabilities
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      o[t] = zero;
+      m[t] = 0.f;
+      l[t] = 0.f;
+    }
+    bool started = false;
     for (int kc = 0; kc < nch; ++kc) {
-      const int flag = cf[kc];
-      if (flag == 0) continue;
+      const uint32_t bits = (uint32_t)__builtin_amdgcn_readlane((int)cml, kc);
+      if (bits == 0) continue;  // every key of the chunk masked: contributes nothing
       const int key = kc * 32 + krow;
       const f16x8 k0 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, kh));
       const f16x8 k1 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, 2 + kh));
-      f32x16 s = mfma32(k0, q0, zero);
-      s = mfma32(k1, q1, s);  // s[i]: key kc*32 + 16*(i/8) + 8*kh + i%8, query q (raw)
-      if (flag == 2) {
+      f32x16 s[T];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] += mb[kc * 32 + 16 * (i >> 3) + 8 * kh + (i & 7)];
+      for (int t = 0; t < T; ++t) {
+        s[t] = mfma32(k0, q0[t], zero);
+        s[t] = mfma32(k1, q1[t], s[t]);  // s[i]: key kc*32 + 16*(i/8) + 8*kh + i%8 (raw)
       }
-      float mx = s[0];
+      if (bits != 0xffffffffu) {
+        const float* mk = mb + kc * 32 + 8 * kh;
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float mn = fmaxf(m, mx);  // finite: the chunk has an unmasked key
-      const float mc = mn * c;
-      const float corr = __builtin_amdgcn_exp2f(m * c - mc);
-      f16x8 pa, pb;
-      float ps = 0.f;
+        for (int i = 0; i < 16; ++i) {
+          const float bias = mk[16 * (i >> 3) + (i & 7)];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[i], c, -mc));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[8 + i], c, -mc));
-        ps += p0 + p1;
-        pa[i] = (f16)p0;
-        pb[i] = (f16)p1;
+          for (int t = 0; t < T; ++t) s[t][i] += bias;
+        }
       }
-      l = l * corr + ps;
-      o *= corr;
+      float mx[T];
+      bool up = false;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float v = fmaxf(fmaxf(s[t][0], s[t][1]), s[t][2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2) v = fmaxf(fmaxf(v, s[t][i]), s[t][i + 1]);
+        v = fmaxf(v, s[t][15]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                         false, false);
+        mx[t] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // finite: a key is unmasked
+        up = up || mx[t] > m[t] + lag;
+      }
+      if (!started) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) m[t] = mx[t];
+        started = true;
+      } else if (__ballot(up)) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float mn = fmaxf(m[t], mx[t]);
+          const float corr = __builtin_amdgcn_exp2f((m[t] - mn) * c);
+          l[t] *= corr;
+          o[t] *= corr;
+          m[t] = mn;
+        }
+      }
       const f16* vrow = Vt + r32 * VLD + kc * 32 + 8 * kh;
-      o = mfma32(*reinterpret_cast<const f16x8*>(vrow), pa, o);
-      o = mfma32(*reinterpret_cast<const f16x8*>(vrow + 16), pb, o);
-      m = mn;
-    }
-    const float lt = l + __shfl_xor(l, 32, kWave);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
-      f16* dst = out + ((size_t)b * seq + q) * hid + h * kHeadDim + 4 * kh;
+      const f16x8 va = *reinterpret_cast<const f16x8*>(vrow);
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(vrow + 16);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f16x4 w;
+      for (int t = 0; t < T; ++t) {
+        const float mc = m[t] * c;
+        f16x8 pa, pb;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
-        *reinterpret_cast<f16x4*>(dst + 8 * j) = w;
+        for (int i = 0; i < 8; ++i) {
+          pa[i] = (f16)__builtin_amdgcn_exp2f(fmaf(s[t][i], c, -mc));
+          pb[i] = (f16)__builtin_amdgcn_exp2f(fmaf(s[t][8 + i], c, -mc));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          l[t] = __builtin_amdgcn_fdot2(f16x2{pa[i], pa[i + 1]}, ones, l[t], false);
+          l[t] = __builtin_amdgcn_fdot2(f16x2{pb[i], pb[i + 1]}, ones, l[t], false);
+        }
+        o[t] = mfma32(va, pa, o[t]);
+        o[t] = mfma32(vb, pb, o[t]);
       }
+    }
+    float inv[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float lt = l[t] + __shfl_xor(l[t], 32, kWave);
+      inv[t] = lt > 0.f ? 1.0f / lt : 0.f;
+    }
+    if constexpr (!(F & 1)) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int q = (wave + NW * (T * g + t)) * 32 + r32;
+        if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
+          f16* dst = out + ((size_t)b * seq + q) * hid + h * kHeadDim + 4 * kh;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            f16x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (f16)(o[t][4 * j + e] * inv[t]);
+            *reinterpret_cast<f16x4*>(dst + 8 * j) = w;
+          }
+        }
+      }
+    } else {
+      // Through this wavefront's LDS tiles, so that each store instruction
+      // writes 16 query rows x 64 contiguous bytes.
+      f16* st = stage + wave * T * 32 * kStageLd;
+      if ((F & 2) && nch <= NW * T) {  // one group per wavefront: reuse the K/V area once all are done
+        if (NW > 1) __syncthreads();
+        st = smem + wave * T * 32 * kStageLd;
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f16x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = (f16)(o[t][4 * j + e] * inv[t]);
+          *reinterpret_cast<f16x4*>(st + (t * 32 + r32) * kStageLd + 8 * j + 4 * kh) = w;
+        }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int row = 16 * p + (lane >> 2), cc = lane & 3;
+          const int q = (wave + NW * (T * g + t)) * 32 + row;
+          const f16x8 w = *reinterpret_cast<const f16x8*>(st + (t * 32 + row) * kStageLd + 8 * cc);
+          if (q < seq)
+            *reinterpret_cast<f16x8*>(out + ((size_t)b * seq + q) * hid + h * kHeadDim + 8 * cc) = w;
+        }
     }
   }
 }
 
-template <int NW>
+template <int NW, int T, int F>
 hipError_t launch_attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
                             int heads, int seq, float c, hipStream_t s) {
+  const int tiles = (seq + 31) / 32;
+  const int staged = !(F & 1) || ((F & 2) && tiles <= NW * T) ? 0 : NW * T;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(attention_kernel<NW>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, (int)attn_lds_bytes(kMaxPos));
+      reinterpret_cast<const void*>(attention_kernel<NW, T, F>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)attn_lds_bytes(kMaxPos, NW * T));
   if (attr != hipSuccess) return attr;
   const int grid = heads * 8 * ((batch + 7) / 8);
-  hipLaunchKernelGGL((attention_kernel<NW>), dim3(grid), dim3(64 * NW), attn_lds_bytes(seq), s,
-                     qkv, mask, merged, batch, seq, heads, c);
+  hipLaunchKernelGGL((attention_kernel<NW, T, F>), dim3(grid), dim3(64 * NW),
+                     attn_lds_bytes(seq, staged), s, qkv, mask, merged, batch, seq, heads, c);
   return hipGetLastError();
 }
+
+}  // namespace
+
+// Workgroup shape by query-tile count (tiles = ceil(seq / 32)).  Up to 7
+// tiles: one tile per wavefront, output staged through the K/V area.  8 tiles:
+// 4 wavefronts x 2 tiles.  16 tiles: 8 x 2.  9-15: 8 x 1 (a 2-tile grouping
+// would leave wavefronts computing empty tiles).
+hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
+                     int seq, float scale, hipStream_t s) {
+  const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
+  const int tiles = (seq + 31) / 32;
+  if (tiles >= 16) return launch_attention<8, 2, 0>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles > 8) return launch_attention<8, 1, 0>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles == 8) return launch_attention<4, 2, 3>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles >= 4) return launch_attention<4, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
+  if (tiles >= 2) return launch_attention<2, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
+  return launch_attention<1, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
+}
+
+namespace {
 
 // ---- unfused pieces with the reference's launcher shapes -------------------
 
@@ -243,15 +391,6 @@ __global__ __launch_bounds__(256) void context_kernel(const f16* __restrict__ pr
 
 }  // namespace
 
-hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
-                     int seq, float scale, hipStream_t s) {
-  const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
-  const int tiles = (seq + 31) / 32;            // 32-query tiles per sequence
-  if (tiles >= 8) return launch_attention<8>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles >= 4) return launch_attention<4>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles >= 2) return launch_attention<2>(qkv, mask, merged, batch, heads, seq, c, s);
-  return launch_attention<1>(qkv, mask, merged, batch, heads, seq, c, s);
-}
 
 hipError_t attention_scores(const f16* qkv, f16* scores, int batch, int heads, int seq,
                             int qkv_stride, int q_off, int k_off_, float scale,

@@ -215,7 +215,8 @@ def _masks(rng, B, S, kind):
 
 @pytest.mark.parametrize("S,kind", [(16, "prefix"), (32, "random"), (48, "empty_row"), (64, "full"),
                                     (80, "prefix"), (128, "random"), (512, "prefix"),
-                                    (512, "empty_row")])
+                                    (512, "empty_row"), (256, "rising"), (512, "rising"),
+                                    (224, "prefix"), (320, "random")])
 def test_fused_attention(torch_cuda, S, kind):
     torch = torch_cuda
     from bbh import engine
@@ -223,7 +224,14 @@ def test_fused_attention(torch_cuda, S, kind):
     rng = np.random.default_rng(S)
     B = 3
     qkv = _h(rng, (B, S, 1152), 1.5)
-    mask = _masks(rng, B, S, kind)
+    if kind == "rising":
+        # Keys whose scores climb along the sequence, by about 10 raw units
+        # per 32-key chunk for sequence 0 (the row max moves a little at every
+        # chunk) and about 100 for sequence 1 (it jumps at every chunk).
+        ramp = np.arange(S, dtype=np.float32)[:, None] * np.array([0.01, 0.1, 0.0])[:, None, None]
+        qkv[..., :384] = np.abs(qkv[..., :384])
+        qkv[..., 384:768] = (qkv[..., 384:768] * 0.1 + ramp).astype(np.float16)
+    mask = _masks(rng, B, S, "full" if kind == "rising" else kind)
     out = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
     engine.launch_attention(to_dev(torch, qkv.reshape(B * S, 1152)), to_dev(torch, mask), out, B, S)
     want = O.attention(qkv.astype(np.float32), mask).reshape(B * S, 384)

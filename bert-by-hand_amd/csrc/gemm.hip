@@ -502,7 +502,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 float v = acc[fm][fn][4 * j + i] + (float)bvs[h][j][i];
-                if (EPI == kGelu) v = gelu_as(v);
+                if (EPI == kGelu) v = gelu_poly(v);
                 o[i] = to_half(v);
               }
             }
@@ -537,7 +537,8 @@ constexpr int NW = 12, THREADS = 64 * NW, K = 384, KS = K / 16, BM = 32, RING = 
 constexpr int TILE = BM * K;                   // halves per A tile
 constexpr int CPW = (BM * K * 2 / 1024) / NW;  // 1 KB copies per wavefront per tile
 constexpr int COLS = NW * 32;                  // output columns per workgroup
-constexpr size_t LDS = (size_t)RING * TILE * sizeof(f16);
+constexpr int kStageLd = 40;  // halves per row of a wavefront's 32 x 32 output block
+constexpr size_t LDS = ((size_t)RING * TILE + (size_t)NW * 32 * kStageLd) * sizeof(f16);
 static_assert((BM * K * 2 / 1024) % NW == 0, "copies per wavefront");
 }  // namespace wres
 
@@ -611,26 +612,38 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
       acc = mfma32(w[st], a[st & 1], acc);
     }
     // acc[i] = D(n0 + 8 (i / 4) + 4 kh + i % 4, m): four 4-column runs of row m.
-    const int m = (mg + i * groups) * BM + r32;
+    const int m0 = (mg + i * groups) * BM;
+    f16* stg = smem + RING * TILE + wave * 32 * kStageLd;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f16x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float v = acc[4 * j + e] + (float)bq[j][e];
-        if (EPI == kGelu) v = gelu_as(v);
+        if (EPI == kGelu) v = gelu_poly(v);
         o[e] = to_half(v);
       }
-      if (m < M) *reinterpret_cast<f16x4*>(out + (size_t)m * N + n0 + 8 * j + 4 * kh) = o;
+      *reinterpret_cast<f16x4*>(stg + r32 * kStageLd + 8 * j + 4 * kh) = o;
+    }
+    // Back out of this wavefront's own LDS block (no barrier needed) as
+    // 16-byte stores, each instruction 16 rows x 64 contiguous bytes: 1.5-2x
+    // the HBM write rate of the 8-byte stores straight from the accumulator
+    // layout (32 rows x 16 bytes per instruction).
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int row = 16 * p + (lane >> 2), cc = lane & 3;
+      const f16x8 v = *reinterpret_cast<const f16x8*>(stg + row * kStageLd + 8 * cc);
+      if (m0 + row < M)
+        *reinterpret_cast<f16x8*>(out + (size_t)(m0 + row) * N + n0 + 8 * cc) = v;
     }
   }
 }
 
 // The weight-resident kernel serves K = 384 and N a multiple of 384, from
-// the M where sweeps on MI355X show it ahead of the tiled kernels: 24576 for
-// FFN1 (N = 1536, where it saves the most L2 traffic per row), 49152 for QKV.
+// the M where sweeps on MI355X show it ahead of the tiled kernels: 16384 for
+// FFN1 (N = 1536, where it saves the most L2 traffic per row), 28672 for QKV.
 bool wres_ok(int M, int N, int K) {
-  return K == wres::K && N % wres::COLS == 0 && M >= (N >= 1536 ? 24576 : 49152);
+  return K == wres::K && N % wres::COLS == 0 && M >= (N >= 1536 ? 16384 : 28672);
 }
 
 template <int EPI>

@@ -75,6 +75,43 @@ def test_linear_rows_identical_across_kernels(torch_cuda, N, gelu):
     assert np.array_equal(_np(big[:m]), _np(small))
 
 
+@pytest.mark.parametrize("M", [4096, 32768])
+def test_gelu_epilogue_accuracy(torch_cuda, M):
+    # The GELU of the FFN1 epilogue against x Phi(x) in float64 over x in
+    # [-14, 14]: W is one-hot (W[n, 0] = 1, exact in fp32 accumulation), so
+    # column n of row m is GELU(x_m + b_n).  M = 4096 runs a tiled kernel,
+    # M = 32768 the weight-resident one.  Bars: the epilogue's own error plus
+    # one fp16 rounding step: 1.1e-5 + half a unit in the last place for
+    # |x| < 3, 2e-4 + half an ulp everywhere.
+    torch = torch_cuda
+    from math import erf, sqrt
+    from bbh import engine
+
+    N, K = 1536, 384
+    x = np.linspace(-14, 14, M).astype(np.float16)
+    A = np.zeros((M, K), np.float16)
+    A[:, 0] = x
+    W = np.zeros((N, K), np.float16)
+    W[:, 0] = 1
+    b = np.zeros(N, np.float16)
+    b[1::2] = 0.25  # half the columns see x + 0.25
+    C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(to_dev(torch, A), to_dev(torch, W), C, M, N, K, bias=to_dev(torch, b),
+                         gelu=True)
+    got = _np(C).astype(np.float64)
+    for col, shift in ((0, 0.0), (1, 0.25)):
+        v = x.astype(np.float64) + shift
+        want = np.array([0.5 * t * (1 + erf(t / sqrt(2))) for t in v])
+        half_ulp = np.abs(want).astype(np.float16).astype(np.float64)
+        half_ulp = np.spacing(half_ulp.astype(np.float16)).astype(np.float64) / 2
+        err = np.abs(got[:, col] - want)
+        small = np.abs(v) < 3
+        assert np.all(err[small] <= 1.1e-5 + half_ulp[small] + 1e-12)
+        assert np.all(err <= 2e-4 + half_ulp)
+    # every column of a row holds the same value as its column of equal bias
+    assert np.array_equal(got[:, 0::2], np.repeat(got[:, :1], N // 2, axis=1))
+
+
 @pytest.mark.parametrize("tag", ["small", "real"])
 def test_linear_reference_kat(torch_cuda, kats, tag):
     # tests/test_matmul.cu: 4x16x8 (any-shape kernel) and 128x384x384 (MFMA)

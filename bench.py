@@ -5,10 +5,11 @@ sentences, lognormal lengths clipped to [5, 64], consecutive batches of 64 in
 seeded order, each padded to round16(longest) (32 batches, eff 32/48/64).
 One step = one pass of bert_embed over all 32 pre-uploaded batches (the
 reference times passes over its corpus the same way, bench/corpus.cu:120-132),
-through bbh_embed_batches: the batches are packed grouped by their padded
-length, so each run of equal-length batches executes as one forward (every
-batch keeps its own padding, so the executed work is unchanged), and the runs
-overlap on N_STREAMS streams.  value = sentences/s over the K timed steps.
+through bbh_embed_packed: only each sentence's valid tokens enter the forward
+(26,857 of the 91,648 padded rows), as one forward on N_STREAMS stream(s).
+The embeddings are those of the padded computation (bbh_embed_batches, which
+runs every padded row) bit for bit; that path is timed too and reported as
+varlen_padded_sentences_per_s.  value = sentences/s over the K timed steps.
 
 The same line also carries, as extra fields: configs[1] (batch 64 x seq 16)
 and configs[2] (batch 64 x seq 128) sent/s (300 timed iterations as
@@ -34,9 +35,10 @@ for _p in (ROOT, os.path.join(ROOT, "bert-by-hand_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-N_STREAMS = 2  # concurrent forwards in the varlen pass (one workspace per stream)
+N_STREAMS = 1  # forwards of the packed varlen pass (one workspace per stream)
+PAD_STREAMS = 2  # concurrent forwards of the padded varlen pass
 POOL_BATCH = 1024  # workspace rows per stream = POOL_BATCH * 64: the 21 batches of
-#                    padded length 48 (64,512 rows) run as one forward
+#                    padded length 48 (64,512 rows) run as one padded forward
 PEAK_FP16_DENSE = 2.5e15  # MI355X published dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
 EPI_OF_OP = {"qkv": "0 (bias)", "ffn1_gelu": "1 (bias+GELU)"}
@@ -189,16 +191,18 @@ def main():
     ws = engine.Workspace(256, 512)
 
     # ---- default workload: varlen mix ------------------------------------
-    # All 32 batches pre-uploaded; bert_embed on every batch, the batches dealt
-    # round-robin over a pool of N_STREAMS streams (one workspace each).
+    # All 32 batches pre-uploaded; bert_embed on every batch through
+    # bbh_embed_packed (valid tokens only) on a pool of N_STREAMS streams.
     batches = synth.varlen_mix()
     n_sent = sum(b[0].shape[0] for b in batches)
     packed = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
+    real_tokens = int(packed.lengths.sum())
+    padded_rows = int(sum(b[0].size for b in batches))
     pool = engine.Pool(N_STREAMS, POOL_BATCH, 64)
     emb_all = torch.empty((packed.rows, 384), dtype=torch.float16, device="cuda")
 
     def step():
-        engine.embed_batches(pool, model, packed, emb=emb_all)
+        engine.embed_packed(pool, model, packed, emb=emb_all)
 
     for _ in range(args.warmup):
         step()
@@ -213,9 +217,21 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = s_ev.elapsed_time(e_ev) / args.steps
     sps = n_sent / (ms_step / 1e3)
-    total_flops = sum(synth.flops_per_forward(b[0].shape[0], b[3]) for b in batches)
-    log(f"varlen ({N_STREAMS} streams): {ms_step:.3f} ms/pass ({wall / args.steps * 1e3:.3f} ms "
-        f"wall), {sps:,.0f} sent/s, {total_flops / (ms_step / 1e3) / 1e12:.1f} TFLOP/s executed")
+    # algorithmic FLOPs over the valid tokens (what the packed pass executes)
+    total_flops = sum(synth.flops_per_forward(1, int(L)) for L in packed.lengths)
+    log(f"varlen packed ({N_STREAMS} stream(s), {real_tokens} of {padded_rows} rows): "
+        f"{ms_step:.3f} ms/pass ({wall / args.steps * 1e3:.3f} ms wall), {sps:,.0f} sent/s, "
+        f"{total_flops / (ms_step / 1e3) / 1e12:.1f} TFLOP/s executed")
+
+    # the padded computation (every padded row) through bbh_embed_batches
+    ppool = engine.Pool(PAD_STREAMS, POOL_BATCH, 64)
+    ms_pad = timed(torch, lambda: engine.embed_batches(ppool, model, packed, emb=emb_all),
+                   args.steps, warmup=args.warmup)
+    ppool.close()
+    pad_flops = sum(synth.flops_per_forward(b[0].shape[0], b[3]) for b in batches)
+    log(f"varlen padded ({PAD_STREAMS} streams, {padded_rows} rows): {ms_pad:.3f} ms/pass, "
+        f"{n_sent / (ms_pad / 1e3):,.0f} sent/s, "
+        f"{pad_flops / (ms_pad / 1e3) / 1e12:.1f} TFLOP/s executed")
 
     # the same workload as one bert_embed per batch on a single stream
     dev = [(torch.from_numpy(i).cuda(), torch.from_numpy(t).cuda(), torch.from_numpy(m).cuda())
@@ -237,34 +253,37 @@ def main():
         "data": "synthetic (seeded random-init MiniLM-L6 weights N(0,0.02), synthetic token ids)",
         "config": {"workload": "varlen mix: 2000 sentences, lognormal(median 12, sigma 0.5) "
                                "lengths clipped to [5,64], consecutive batches of 64 padded to "
-                               "round16(max); one step = bert_embed over all 32 batches via "
-                               "bbh_embed_batches, batches packed grouped by padded length so "
-                               "each equal-length run is one forward (runs of 8/21/3 batches "
-                               f"at seq 32/48/64), runs on {N_STREAMS} streams",
+                               f"round16(max) ({padded_rows} padded rows, {real_tokens} valid "
+                               "tokens); one step = bert_embed over all 32 batches via "
+                               "bbh_embed_packed: only valid tokens enter the forward (one "
+                               f"forward of {real_tokens} rows on {N_STREAMS} stream(s)); the "
+                               "embeddings equal the padded computation's (bbh_embed_batches) "
+                               "bit for bit",
                    "streams": N_STREAMS, "pool_rows_per_stream": POOL_BATCH * 64,
                    "model": "MiniLM-L6 (6 layers, hidden 384, 12x32 heads, FFN 1536)",
-                   "global_batch": 64, "seq_len": "32/48/64 (mean eff 45.8)",
+                   "global_batch": 64,
+                   "seq_len": f"5..64 valid ({real_tokens / n_sent:.1f} mean), padded 32/48/64",
                    "parallelism": "single GPU"},
         "ms_per_sentence": round(ms_step / n_sent, 6),
+        "varlen_padded_sentences_per_s": round(n_sent / (ms_pad / 1e3), 1),
+        "varlen_padded_streams": PAD_STREAMS,
         "varlen_single_stream_sentences_per_s": round(n_sent / (ms1 / 1e3), 1),
         "executed_tflops": round(total_flops / (ms_step / 1e3) / 1e12, 2),
     }
 
     # ---- dominant kernel of the default workload ---------------------------
-    # The same packed runs again, through a one-stream pool with per-launch
+    # The same packed pass again, through a one-stream pool with per-launch
     # timing on: a pair of HIP events on the pool stream around every op
-    # launch.  One stream, so each event pair brackets that kernel alone (in
-    # the two-stream pass the other stream's kernels share the GPU and
-    # stretch every launch).  The dominant kernel is the (op, tile) class with
-    # the largest summed time per pass.
+    # launch, so each event pair brackets that kernel alone.  The dominant
+    # kernel is the (op, tile) class with the largest summed time per pass.
     tpool = engine.Pool(1, POOL_BATCH, 64)
-    n_ops = 32 * 6 * 5
+    n_ops = 6 * 5
     tpool.timing(n_ops * args.steps)
-    engine.embed_batches(tpool, model, packed, emb=emb_all)  # warm (records overwritten below)
+    engine.embed_packed(tpool, model, packed, emb=emb_all)  # warm (records overwritten below)
     torch.cuda.synchronize()
     tpool.timing(n_ops * args.steps)
     for _ in range(args.steps):
-        engine.embed_batches(tpool, model, packed, emb=emb_all)
+        engine.embed_packed(tpool, model, packed, emb=emb_all)
     recs = tpool.timing_read()
     tpool.timing(0)
     tpool.close()
@@ -275,10 +294,10 @@ def main():
         c["ms"] += r["ms"]
         c["n"] += 1
         c["m"].add(r["m"])
-        if r["op"] == "attention":
-            B, S, H = r["m"], r["n"], r["k"]
-            c["flops"] += 4.0 * B * H * 32 * S * S
-            c["bytes"] += B * S * (3 * 384 + 384) * 2.0
+        if r["op"] == "attention":  # packed: per sentence at its own length
+            lens = packed.lengths.astype(np.float64)
+            c["flops"] += 4.0 * r["k"] * 32 * float((lens * lens).sum())
+            c["bytes"] += float(lens.sum()) * (3 * 384 + 384) * 2.0
         else:
             M, N, K = r["m"], r["n"], r["k"]
             c["flops"] += 2.0 * M * N * K
@@ -371,8 +390,17 @@ def main():
             gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
             gemm_ms += t
             gemm_flops += f
+        # the same batch through bbh_embed_packed (valid tokens only: lengths
+        # uniform in [256, 512], so about 3/4 of the padded rows)
+        pk5 = engine.PackedBatches([synth.long_batch()])
+        pool5 = engine.Pool(1, 256, 512)
+        ms_p5 = timed(torch, lambda: engine.embed_packed(pool5, model, pk5, emb=emb5), 10,
+                      warmup=2)
+        pool5.close()
         out["cfg5_b256_s512"] = {
             "sentences_per_s": round(256 / (ms / 1e3), 1), "ms_per_forward": round(ms, 3),
+            "packed_sentences_per_s": round(256 / (ms_p5 / 1e3), 1),
+            "packed_valid_tokens": int(pk5.lengths.sum()),
             "tflops": round(synth.flops_per_forward(256, 512) / (ms / 1e3) / 1e12, 2),
             "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
             "per_gemm_frac": gem}

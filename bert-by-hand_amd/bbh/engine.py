@@ -221,6 +221,14 @@ class PackedBatches:
         cat = lambda k: torch.from_numpy(np.concatenate([np.asarray(b[k]).reshape(-1) for b in batches]).astype(np.int32)).cuda()  # noqa: E731
         self.ids, self.types, self.mask = cat(0), cat(1), cat(2)
         self.n = n
+        # per sentence (packed order): number of valid tokens, and whether
+        # every mask is right-padding (ones then zeros), which embed_packed needs
+        rows_mask = [np.asarray(b[2]).reshape(int(b[0].shape[0]), -1) != 0 for b in batches]
+        self.lengths = (np.concatenate([m.sum(axis=1) for m in rows_mask]).astype(np.int32)
+                        if n else np.zeros(0, np.int32))
+        self.right_padded = all(
+            bool(np.all(m == (np.arange(m.shape[1])[None, :] < m.sum(axis=1)[:, None])))
+            for m in rows_mask)
         # packed sentence row -> input sentence row
         in_sizes = np.zeros(n, np.int64)
         in_sizes[self.order] = self.sizes
@@ -245,6 +253,21 @@ def embed_batches(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
     call("bbh_embed_batches", pool.handle, w.handle, _ptr(packed.ids), _ptr(packed.types),
          _ptr(packed.mask), p(packed.tok_offsets), p(packed.sizes), p(packed.seqs),
+         p(packed.emb_rows), _ptr(emb), packed.n, _stream(stream))
+    return emb
+
+
+def embed_packed(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=None):
+    """embed_batches without the padding rows: only each sentence's valid
+    tokens enter the forward (bbh_embed_packed).  Needs right-padded masks."""
+    torch = _torch()
+    if not packed.right_padded:
+        raise ValueError("embed_packed needs right-padded masks (ones, then zeros)")
+    if emb is None:
+        emb = torch.empty((packed.rows, HIDDEN), dtype=torch.float16, device="cuda")
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    call("bbh_embed_packed", pool.handle, w.handle, _ptr(packed.ids), _ptr(packed.types),
+         p(packed.tok_offsets), p(packed.sizes), p(packed.seqs), p(packed.lengths),
          p(packed.emb_rows), _ptr(emb), packed.n, _stream(stream))
     return emb
 

@@ -77,16 +77,25 @@ constexpr float kLazy = 8.f;
 // take tile groups round robin.
 // F: 1 stage the output through LDS, 2 put that staging in the K/V area
 // (one tile group per wavefront).
-template <int NW, int T, int F>
+// VL: packed sentences (sents[b] gives the rows and length; every token is
+// valid, `mask` and `seq` are unused).
+template <int NW, int T, int F, bool VL = false>
 __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
     const f16* __restrict__ qkv, const int32_t* __restrict__ mask, f16* __restrict__ out,
-    int batch, int seq, int heads, float c) {
+    int batch, int seq, int heads, float c, const PackedSentence* __restrict__ sents) {
   HIP_DYNAMIC_SHARED(f16, smem);
   // (sequence, head) of this workgroup; all heads of a sequence go to one XCD
   // (workgroup id % 8) back to back, so its QKV rows are fetched into one L2.
   const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
   const int b = (k / heads) * 8 + x, h = k % heads;
   if (b >= batch) return;
+  size_t row0 = (size_t)b * seq;  // first hidden row of the sentence
+  if constexpr (VL) {
+    const PackedSentence sn = sents[b];
+    seq = sn.len;
+    row0 = (size_t)sn.row;
+    if (seq == 0) return;  // no tokens: nothing to attend, no rows to write
+  }
   const int seqp = (seq + 31) & ~31, nch = seqp >> 5, VLD = seqp + 8;
   f16* Ks = smem;                                              // [seqp][32]
   f16* Vt = Ks + seqp * 32;                                    // [32][VLD]
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
   uint32_t* cm = reinterpret_cast<uint32_t*>(mb + seqp);       // [nch]: unmasked-key bitmaps
   f16* stage = reinterpret_cast<f16*>(cm + ((nch + 3) & ~3));  // [NW*T][32][kStageLd]
   const int hid = heads * kHeadDim, ld = 3 * hid;
-  const f16* base = qkv + (size_t)b * seq * ld + h * kHeadDim;
+  const f16* base = qkv + row0 * ld + h * kHeadDim;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r32 = lane & 31, kh = lane >> 5;
   constexpr int NT = 64 * NW;
 
@@ -136,12 +145,12 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
     }
   }
   if (wave == NW - 1) {  // key bias and bitmaps of unmasked keys, 64 keys per ballot
-    const int32_t* mrow = mask + (size_t)b * seq;
+    const int32_t* mrow = VL ? nullptr : mask + (size_t)b * seq;
     int mv[kMaxPos / 64];
 #pragma unroll
     for (int j = 0; j < kMaxPos / 64; ++j) {
       const int key = 64 * j + lane;
-      mv[j] = (64 * j < seq && key < seq) ? mrow[key] : 0;
+      mv[j] = (64 * j < seq && key < seq) ? (VL ? 1 : mrow[key]) : 0;
     }
 #pragma unroll
     for (int j = 0; j < kMaxPos / 64; ++j) {
@@ -250,7 +259,7 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
       for (int t = 0; t < T; ++t) {
         const int q = (wave + NW * (T * g + t)) * 32 + r32;
         if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
-          f16* dst = out + ((size_t)b * seq + q) * hid + h * kHeadDim + 4 * kh;
+          f16* dst = out + (row0 + q) * hid + h * kHeadDim + 4 * kh;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             f16x4 w;
@@ -285,43 +294,66 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
           const int q = (wave + NW * (T * g + t)) * 32 + row;
           const f16x8 w = *reinterpret_cast<const f16x8*>(st + (t * 32 + row) * kStageLd + 8 * cc);
           if (q < seq)
-            *reinterpret_cast<f16x8*>(out + ((size_t)b * seq + q) * hid + h * kHeadDim + 8 * cc) = w;
+            *reinterpret_cast<f16x8*>(out + (row0 + q) * hid + h * kHeadDim + 8 * cc) = w;
         }
     }
   }
+  // A packed sentence may have fewer query tiles than the workgroup has
+  // wavefronts; those wavefronts still take part in the staging barrier.
+  if constexpr (VL && (F & 2)) {
+    if (NW > 1 && nch <= NW * T && wave >= nch) __syncthreads();
+  }
 }
 
-template <int NW, int T, int F>
+template <int NW, int T, int F, bool VL = false>
 hipError_t launch_attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
-                            int heads, int seq, float c, hipStream_t s) {
-  const int tiles = (seq + 31) / 32;
+                            int heads, int seq, float c, hipStream_t s,
+                            const PackedSentence* sents = nullptr) {
+  const int tiles = (seq + 31) / 32;  // for VL: of the longest sentence
   const int staged = !(F & 1) || ((F & 2) && tiles <= NW * T) ? 0 : NW * T;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(attention_kernel<NW, T, F>),
+      reinterpret_cast<const void*>(attention_kernel<NW, T, F, VL>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)attn_lds_bytes(kMaxPos, NW * T));
   if (attr != hipSuccess) return attr;
   const int grid = heads * 8 * ((batch + 7) / 8);
-  hipLaunchKernelGGL((attention_kernel<NW, T, F>), dim3(grid), dim3(64 * NW),
-                     attn_lds_bytes(seq, staged), s, qkv, mask, merged, batch, seq, heads, c);
+  hipLaunchKernelGGL((attention_kernel<NW, T, F, VL>), dim3(grid), dim3(64 * NW),
+                     attn_lds_bytes(seq, staged), s, qkv, mask, merged, batch, seq, heads, c,
+                     sents);
   return hipGetLastError();
 }
-
-}  // namespace
 
 // Workgroup shape by query-tile count (tiles = ceil(seq / 32)).  Up to 7
 // tiles: one tile per wavefront, output staged through the K/V area.  8 tiles:
 // 4 wavefronts x 2 tiles.  16 tiles: 8 x 2.  9-15: 8 x 1 (a 2-tile grouping
-// would leave wavefronts computing empty tiles).
-hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
-                     int seq, float scale, hipStream_t s) {
+// would leave wavefronts computing empty tiles).  For packed sentences the
+// longest one sets the shape.
+template <bool VL>
+hipError_t attention_any(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
+                         int seq, float scale, hipStream_t s, const PackedSentence* sents) {
   const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
   const int tiles = (seq + 31) / 32;
-  if (tiles >= 16) return launch_attention<8, 2, 0>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles > 8) return launch_attention<8, 1, 0>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles == 8) return launch_attention<4, 2, 3>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles >= 4) return launch_attention<4, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
-  if (tiles >= 2) return launch_attention<2, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
-  return launch_attention<1, 1, 3>(qkv, mask, merged, batch, heads, seq, c, s);
+#define BBH_ATT(NW, T, F) \
+  launch_attention<NW, T, F, VL>(qkv, mask, merged, batch, heads, seq, c, s, sents)
+  if (tiles >= 16) return BBH_ATT(8, 2, 0);
+  if (tiles > 8) return BBH_ATT(8, 1, 0);
+  if (tiles == 8) return BBH_ATT(4, 2, 3);
+  if (tiles >= 4) return BBH_ATT(4, 1, 3);
+  if (tiles >= 2) return BBH_ATT(2, 1, 3);
+  return BBH_ATT(1, 1, 3);
+#undef BBH_ATT
+}
+
+}  // namespace
+
+hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch, int heads,
+                     int seq, float scale, hipStream_t s) {
+  return attention_any<false>(qkv, mask, merged, batch, heads, seq, scale, s, nullptr);
+}
+
+hipError_t attention_packed(const f16* qkv, const PackedSentence* sents, int n, f16* merged,
+                            int heads, int max_len, float scale, hipStream_t s) {
+  if (n == 0 || max_len == 0) return hipSuccess;
+  return attention_any<true>(qkv, nullptr, merged, n, heads, max_len, scale, s, sents);
 }
 
 namespace {

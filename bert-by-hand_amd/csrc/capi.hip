@@ -121,6 +121,7 @@ struct bbh_workspace {
   void* blob = nullptr;
   size_t bytes = 0;
   f16 *qkv, *ctx, *attn_out, *inter, *ping, *pong;
+  bbh::PackedSentence* sents;  // plan of a packed forward: up to `rows` sentences
 };
 
 namespace {
@@ -283,15 +284,27 @@ struct Segment {
   size_t row;
 };
 
+// A packed forward: n sentences (their plan in ws->sents), the longest max_len.
+struct Packed {
+  int n, max_len;
+};
+
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
                                const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
-                               OpTimer* t = nullptr) {
+                               OpTimer* t = nullptr, const Packed* pk = nullptr) {
   const int H = BBH_HIDDEN;
   BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H), 0, M, 3 * H, H, 0.f}, [&] {
     return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
                                   bbh::Act::kNone, s),
                         "qkv gemm");
   }));
+  if (pk) {
+    BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, pk->n, pk->max_len, BBH_NUM_HEADS, 0.f}, [&] {
+      return check_launch(bbh::attention_packed(ws->qkv, ws->sents, pk->n, ws->ctx, BBH_NUM_HEADS,
+                                                pk->max_len, kScale, s),
+                          "attention (packed)");
+    }));
+  }
   for (int g = 0; g < n_segs; ++g) {
     const Segment& sg = segs[g];
     BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, sg.batch, sg.seq, BBH_NUM_HEADS, 0.f}, [&] {
@@ -357,6 +370,25 @@ bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t*
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
     BBH_TRY(run_attention_block(ws, m->layers[i], cur, segs, n_segs, ws->attn_out, M, s, t));
+    BBH_TRY(run_ffn_rows(ws, m->layers[i], ws->attn_out, nxt, M, s, t));
+    cur = nxt;
+  }
+  return BBH_OK;
+}
+
+// Embeddings + 6 layers over a packed forward of M rows (plan in ws->sents).
+bbh_status run_encode_packed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
+                             const int32_t* types, const Packed& pk, int M, f16* final_out,
+                             hipStream_t s, OpTimer* t = nullptr) {
+  BBH_TRY(check_launch(bbh::embedding_ln_packed(ids, types, m->word, m->pos, m->type, m->emb_g,
+                                                m->emb_b, ws->ping, ws->sents, pk.n,
+                                                BBH_LAYER_NORM_EPS, s),
+                       "embedding+ln (packed)"));
+  if (M == 0) return BBH_OK;
+  f16* cur = ws->ping;
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
+    BBH_TRY(run_attention_block(ws, m->layers[i], cur, nullptr, 0, ws->attn_out, M, s, t, &pk));
     BBH_TRY(run_ffn_rows(ws, m->layers[i], ws->attn_out, nxt, M, s, t));
     cur = nxt;
   }
@@ -691,7 +723,8 @@ size_t bbh_workspace_bytes(int max_batch, int max_seq) {
   if (max_batch < 1 || max_seq < 1) return 0;
   const size_t rows = (size_t)max_batch * max_seq;
   const size_t H = BBH_HIDDEN;
-  return align256(rows * 3 * H * 2) + align256(rows * BBH_FFN_DIM * 2) + 4 * align256(rows * H * 2);
+  return align256(rows * 3 * H * 2) + align256(rows * BBH_FFN_DIM * 2) + 4 * align256(rows * H * 2) +
+         align256(rows * sizeof(bbh::PackedSentence));
 }
 
 bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out) {
@@ -728,6 +761,7 @@ bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out)
   ws->attn_out = take(rows * H * 2);
   ws->ping = take(rows * H * 2);
   ws->pong = take(rows * H * 2);
+  ws->sents = reinterpret_cast<bbh::PackedSentence*>(take(rows * sizeof(bbh::PackedSentence)));
   *out = ws;
   return BBH_OK;
 }
@@ -825,10 +859,24 @@ struct bbh_pool {
   hipEvent_t fork = nullptr;
   std::vector<bbh_workspace*> ws;
   OpTimer* timer = nullptr;  // bbh_pool_timing
+  // bbh_embed_packed: plans go host -> device from pinned memory, two slots
+  // used alternately by consecutive calls; a slot is rewritten only after the
+  // copies that last read it (events per stream) have completed.
+  struct Slot {
+    bbh::PackedSentence* host = nullptr;
+    size_t cap = 0;  // entries
+    std::vector<hipEvent_t> copied;
+    std::vector<bool> pending;
+  } slot[2];
+  int next_slot = 0;
 };
 
 static void pool_release(bbh_pool* p) {
   for (auto st : p->streams) (void)hipStreamSynchronize(st);
+  for (auto& sl : p->slot) {
+    for (auto e : sl.copied) (void)hipEventDestroy(e);
+    if (sl.host) (void)hipHostFree(sl.host);
+  }
   delete p->timer;
   for (auto w : p->ws) bbh_workspace_free(w);
   for (auto e : p->done) (void)hipEventDestroy(e);
@@ -869,6 +917,16 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
       return fail(st2, msg);
     }
     p->ws.push_back(w);
+    for (auto& sl : p->slot) {
+      hipEvent_t ce;
+      e = hipEventCreateWithFlags(&ce, hipEventDisableTiming);
+      if (e != hipSuccess) {
+        pool_release(p);
+        return hip_fail(e, "hipEventCreate");
+      }
+      sl.copied.push_back(ce);
+      sl.pending.push_back(false);
+    }
   }
   *out = p;
   return BBH_OK;
@@ -1001,6 +1059,113 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
                                                pool->streams[j]),
                            "pool+normalize"));
     }
+  }
+  for (int j = 0; j < used; ++j) {
+    BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
+    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
+  }
+  return BBH_OK;
+}
+
+bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* ids,
+                            const int32_t* types, const int64_t* tok_offsets,
+                            const int* batch_sizes, const int* seqs, const int32_t* lengths,
+                            const int64_t* emb_rows, void* emb, int n_batches,
+                            bbh_stream_t stream) {
+  if (!pool || !m || !ids || !types || !tok_offsets || !batch_sizes || !seqs || !lengths ||
+      !emb_rows || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed_packed: null argument");
+  if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
+  if (!aligned(emb, 4)) return misaligned("bbh_embed_packed emb");
+  const int n = (int)pool->streams.size();
+  const size_t cap = pool->ws[0]->rows;  // tokens and sentences per forward
+  // The sentences in batch order, validated before anything is enqueued.
+  std::vector<bbh::PackedSentence> all;
+  size_t k = 0, total = 0;
+  for (int i = 0; i < n_batches; ++i) {
+    const std::string at = "batch " + std::to_string(i) + ": ";
+    if (batch_sizes[i] < 0) return fail(BBH_ERR_INVALID_ARG, at + "negative batch size");
+    if (seqs[i] < 1 || seqs[i] > BBH_MAX_POSITION)
+      return fail(BBH_ERR_CAPACITY, at + "seq must be in [1, 512]");
+    if (tok_offsets[i] < 0 || emb_rows[i] < 0)
+      return fail(BBH_ERR_INVALID_ARG, at + "negative offset");
+    for (int j = 0; j < batch_sizes[i]; ++j, ++k) {
+      const int len = lengths[k];
+      if (len < 0 || len > seqs[i])
+        return fail(BBH_ERR_INVALID_ARG, at + "sentence " + std::to_string(j) + " length " +
+                                             std::to_string(len) + " outside [0, seq]");
+      all.push_back({tok_offsets[i] + (int64_t)j * seqs[i], emb_rows[i] + j, 0, len});
+      total += (size_t)len;
+    }
+  }
+  const size_t n_sent = all.size();
+  if (n_sent == 0) return BBH_OK;
+  // Forwards: consecutive sentences, about total / n tokens each (one per
+  // stream), none over a workspace's rows in tokens or in sentences.
+  const size_t target = std::max<size_t>(1, (total + n - 1) / n);
+  std::vector<size_t> cut{0};  // first sentence of each forward
+  size_t toks = 0;
+  for (size_t i = 0; i < n_sent; ++i) {
+    const size_t len = (size_t)all[i].len;
+    if (i > cut.back() && (toks + len > cap || i - cut.back() >= cap ||
+                           (toks >= target && (int)cut.size() < n))) {
+      cut.push_back(i);
+      toks = 0;
+    }
+    toks += len;
+  }
+  cut.push_back(n_sent);
+  const int n_fwd = (int)cut.size() - 1;
+  // Plan rows and the pinned slot.
+  bbh_pool::Slot& sl = pool->slot[pool->next_slot];
+  pool->next_slot ^= 1;
+  for (int j = 0; j < n; ++j)
+    if (sl.pending[j]) {
+      BBH_HIP(hipEventSynchronize(sl.copied[j]), "hipEventSynchronize(plan slot)");
+      sl.pending[j] = false;
+    }
+  if (sl.cap < n_sent) {
+    if (sl.host) BBH_HIP(hipHostFree(sl.host), "hipHostFree");
+    sl.host = nullptr;
+    sl.cap = 0;
+    BBH_HIP(hipHostMalloc(reinterpret_cast<void**>(&sl.host), n_sent * sizeof(bbh::PackedSentence),
+                          hipHostMallocDefault),
+            "hipHostMalloc(plan)");
+    sl.cap = n_sent;
+  }
+  for (int f = 0; f < n_fwd; ++f) {
+    int32_t row = 0;
+    for (size_t i = cut[f]; i < cut[f + 1]; ++i) {
+      all[i].row = row;
+      row += all[i].len;
+    }
+  }
+  std::copy(all.begin(), all.end(), sl.host);
+  const hipStream_t caller = S(stream);
+  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
+  const int used = n_fwd < n ? n_fwd : n;
+  for (int j = 0; j < used; ++j)
+    BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
+  for (int f = 0; f < n_fwd; ++f) {
+    const int j = f % n;
+    const hipStream_t st = pool->streams[j];
+    bbh_workspace* w = pool->ws[j];
+    const size_t first = cut[f], cnt = cut[f + 1] - cut[f];
+    int M = 0, max_len = 0;
+    for (size_t i = first; i < first + cnt; ++i) {
+      M += all[i].len;
+      max_len = std::max(max_len, all[i].len);
+    }
+    BBH_HIP(hipMemcpyAsync(w->sents, sl.host + first, cnt * sizeof(bbh::PackedSentence),
+                           hipMemcpyHostToDevice, st),
+            "hipMemcpyAsync(plan)");
+    BBH_HIP(hipEventRecord(sl.copied[j], st), "hipEventRecord(plan copied)");
+    sl.pending[j] = true;
+    const Packed pk{(int)cnt, max_len};
+    BBH_TRY(run_encode_packed(w, m, ids, types, pk, M, w->attn_out, st, pool->timer));
+    BBH_TRY(check_launch(bbh::pool_normalize_packed(w->attn_out, w->sents, (int)cnt,
+                                                    static_cast<f16*>(emb), st),
+                         "pool+normalize (packed)"));
   }
   for (int j = 0; j < used; ++j) {
     BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");

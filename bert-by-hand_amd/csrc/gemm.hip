@@ -641,9 +641,9 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
 
 // The weight-resident kernel serves K = 384 and N a multiple of 384, from
 // the M where sweeps on MI355X show it ahead of the tiled kernels: 16384 for
-// FFN1 (N = 1536, where it saves the most L2 traffic per row), 28672 for QKV.
+// FFN1 (N = 1536, where it saves the most L2 traffic per row), 24576 for QKV.
 bool wres_ok(int M, int N, int K) {
-  return K == wres::K && N % wres::COLS == 0 && M >= (N >= 1536 ? 16384 : 28672);
+  return K == wres::K && N % wres::COLS == 0 && M >= (N >= 1536 ? 16384 : 24576);
 }
 
 template <int EPI>

@@ -11,6 +11,14 @@ namespace bbh {
 
 enum class Act { kNone, kGelu };
 
+// One sentence of a packed forward: its `len` valid tokens (the leading ones
+// of its padded row, ids/types at tok .. tok + len - 1) occupy hidden rows
+// row .. row + len - 1, and its embedding goes to row out_row of the output.
+struct PackedSentence {
+  int64_t tok, out_row;
+  int32_t row, len;
+};
+
 // C(M,N) = A(M,K) . W(N,K)^T [+ bias] [GELU].  True when the MFMA path takes
 // the shape (N % 64 == 0, K % 64 == 0); otherwise the plain tiled kernel runs.
 bool gemm_mfma_ok(int N, int K);
@@ -34,6 +42,11 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
 hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
                      int heads, int seq, float scale, hipStream_t s);
 
+// The same over packed sentences (no padding rows, no mask): workgroup (s, h)
+// attends over rows sents[s].row .. + len.  max_len bounds every len.
+hipError_t attention_packed(const f16* qkv, const PackedSentence* sents, int n, f16* merged,
+                            int heads, int max_len, float scale, hipStream_t s);
+
 // Reference-shaped attention pieces (unfused): scores, masked softmax, context.
 hipError_t attention_scores(const f16* qkv, f16* scores, int batch, int heads, int seq,
                             int qkv_stride, int q_off, int k_off, float scale,
@@ -56,6 +69,15 @@ hipError_t embedding_ln(const int32_t* ids, const int32_t* types, const f16* wor
                         const f16* pos, const f16* type, const f16* gamma,
                         const f16* beta, f16* out, int batch, int seq, float eps,
                         hipStream_t s);
+
+// Embedding + LayerNorm and mean pool + L2 normalise over packed sentences
+// (one workgroup per sentence).
+hipError_t embedding_ln_packed(const int32_t* ids, const int32_t* types, const f16* word,
+                               const f16* pos, const f16* type, const f16* gamma,
+                               const f16* beta, f16* out, const PackedSentence* sents, int n,
+                               float eps, hipStream_t s);
+hipError_t pool_normalize_packed(const f16* hidden, const PackedSentence* sents, int n,
+                                 f16* out, hipStream_t s);
 
 // Masked mean pool, L2 normalise, and the two fused.
 hipError_t mean_pool(const f16* hidden, const int32_t* mask, f16* out, int batch,

@@ -99,6 +99,28 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(const f16* x, const f16
 
 __device__ __forceinline__ int clamp_id(int v, int n) { return v < 0 ? 0 : (v >= n ? n - 1 : v); }
 
+// One wavefront's row: LN(word[id] + pos[p] + type[tt]), the sum kept in fp32.
+__device__ __forceinline__ void embed_row(int id_raw, int tt_raw, int p, const f16* word,
+                                          const f16* pos, const f16* type, const f16* gamma,
+                                          const f16* beta, f16* dst, float eps, int lane) {
+  const int id = clamp_id(id_raw, kVocab), tt = clamp_id(tt_raw, kTypes);
+  const f16* wr = word + (size_t)id * kHidden;
+  const f16* pr = pos + (size_t)p * kHidden;
+  const f16* tr = type + (size_t)tt * kHidden;
+  float v[6];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int c = 2 * lane + 128 * j;
+    const f16x2 a = *reinterpret_cast<const f16x2*>(wr + c);
+    const f16x2 q = *reinterpret_cast<const f16x2*>(pr + c);
+    const f16x2 t = *reinterpret_cast<const f16x2*>(tr + c);
+    v[2 * j] = (float)a[0] + (float)q[0] + (float)t[0];
+    v[2 * j + 1] = (float)a[1] + (float)q[1] + (float)t[1];
+  }
+  ln_row384(v, eps);
+  store_affine384(dst, v, gamma, beta, lane);
+}
+
 // out[row] = LN(word[id] + pos[row % seq] + type[tt]) (src/model/forward.cu:28-31;
 // gather as src/kernels/embedding.cu:20-30, sum kept in fp32 into the LN).
 __global__ __launch_bounds__(256) void embedding_ln_kernel(
@@ -108,22 +130,22 @@ __global__ __launch_bounds__(256) void embedding_ln_kernel(
     int seq, float eps) {
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
-  const int id = clamp_id(ids[row], kVocab), tt = clamp_id(types[row], kTypes);
-  const f16* wr = word + (size_t)id * kHidden;
-  const f16* pr = pos + (size_t)(row % seq) * kHidden;
-  const f16* tr = type + (size_t)tt * kHidden;
-  float v[6];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int c = 2 * lane + 128 * j;
-    const f16x2 a = *reinterpret_cast<const f16x2*>(wr + c);
-    const f16x2 p = *reinterpret_cast<const f16x2*>(pr + c);
-    const f16x2 t = *reinterpret_cast<const f16x2*>(tr + c);
-    v[2 * j] = (float)a[0] + (float)p[0] + (float)t[0];
-    v[2 * j + 1] = (float)a[1] + (float)p[1] + (float)t[1];
-  }
-  ln_row384(v, eps);
-  store_affine384(out + (size_t)row * kHidden, v, gamma, beta, lane);
+  embed_row(ids[row], types[row], row % seq, word, pos, type, gamma, beta,
+            out + (size_t)row * kHidden, eps, lane);
+}
+
+// The packed layout: workgroup s embeds sentence s's len tokens, wavefront w
+// positions w, w + 4, ...
+__global__ __launch_bounds__(256) void embedding_ln_packed_kernel(
+    const int32_t* __restrict__ ids, const int32_t* __restrict__ types,
+    const f16* __restrict__ word, const f16* __restrict__ pos, const f16* __restrict__ type,
+    const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* __restrict__ out,
+    const PackedSentence* __restrict__ sents, float eps) {
+  const PackedSentence sn = sents[blockIdx.x];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int p = wave; p < sn.len; p += kRowsPerBlock)
+    embed_row(ids[sn.tok + p], types[sn.tok + p], p, word, pos, type, gamma, beta,
+              out + (size_t)(sn.row + p) * kHidden, eps, lane);
 }
 
 // Plain gather-sum, any hidden size (src/kernels/embedding.cu:8-31).
@@ -142,25 +164,24 @@ __global__ __launch_bounds__(256) void embedding_kernel(
 }
 
 // One workgroup per sentence: the four wavefronts sum disjoint sets of tokens
-// (rows w, w+4, ...) of the masked mean, combine through LDS, then wave 0
+// (positions w, w+4, ...) of the masked mean, combine through LDS, then wave 0
 // divides by max(count, 1) (src/kernels/pooling.cu:21-31) and scales by
-// 1 / max(||x||, 1e-12) (src/kernels/normalize.cu:7,29-30).
-__global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restrict__ hidden,
-                                                             const int32_t* __restrict__ mask,
-                                                             f16* __restrict__ out, int seq) {
+// 1 / max(||x||, 1e-12) (src/kernels/normalize.cu:7,29-30).  `row(p)` is the
+// hidden row of position p, or null for a masked position.
+template <class RowOf>
+__device__ __forceinline__ void pool_normalize_body(int seq, RowOf row, f16* __restrict__ dst) {
   __shared__ float part[4][kHidden];
   __shared__ int cnt_part[4];
-  const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const f16* hb = hidden + (size_t)b * seq * kHidden;
-  const int32_t* mb = mask + (size_t)b * seq;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int cnt = 0;
   for (int s = wave; s < seq; s += 4) {
-    if (mb[s] == 0) continue;
+    const f16* hr = row(s);
+    if (!hr) continue;
     ++cnt;
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      const f16x2 a = *reinterpret_cast<const f16x2*>(hb + (size_t)s * kHidden + 2 * lane + 128 * j);
+      const f16x2 a = *reinterpret_cast<const f16x2*>(hr + 2 * lane + 128 * j);
       acc[2 * j] += (float)a[0];
       acc[2 * j + 1] += (float)a[1];
     }
@@ -190,8 +211,29 @@ __global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restri
     f16x2 o;
     o[0] = (f16)(v[2 * j] * inv);
     o[1] = (f16)(v[2 * j + 1] * inv);
-    *reinterpret_cast<f16x2*>(out + (size_t)b * kHidden + 2 * lane + 128 * j) = o;
+    *reinterpret_cast<f16x2*>(dst + 2 * lane + 128 * j) = o;
   }
+}
+
+__global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restrict__ hidden,
+                                                             const int32_t* __restrict__ mask,
+                                                             f16* __restrict__ out, int seq) {
+  const int b = blockIdx.x;
+  const f16* hb = hidden + (size_t)b * seq * kHidden;
+  const int32_t* mb = mask + (size_t)b * seq;
+  pool_normalize_body(
+      seq, [&](int p) { return mb[p] != 0 ? hb + (size_t)p * kHidden : nullptr; },
+      out + (size_t)b * kHidden);
+}
+
+// Packed sentences: position p of sentence s is hidden row sents[s].row + p.
+__global__ __launch_bounds__(256) void pool_normalize_packed_kernel(
+    const f16* __restrict__ hidden, const PackedSentence* __restrict__ sents,
+    f16* __restrict__ out) {
+  const PackedSentence sn = sents[blockIdx.x];
+  const f16* hb = hidden + (size_t)sn.row * kHidden;
+  pool_normalize_body(
+      sn.len, [&](int p) { return hb + (size_t)p * kHidden; }, out + (size_t)sn.out_row * kHidden);
 }
 
 // out[b, d] = masked mean over seq, any dim (src/kernels/pooling.cu:8-32).
@@ -302,6 +344,23 @@ hipError_t gelu(f16* x, size_t n, hipStream_t s) {
   if (rest)
     hipLaunchKernelGGL(gelu1_kernel, dim3((unsigned)((rest + 255) / 256)), dim3(256), 0, s,
                        x + n8 * 8, rest);
+  return hipGetLastError();
+}
+
+hipError_t embedding_ln_packed(const int32_t* ids, const int32_t* types, const f16* word,
+                               const f16* pos, const f16* type, const f16* gamma,
+                               const f16* beta, f16* out, const PackedSentence* sents, int n,
+                               float eps, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(embedding_ln_packed_kernel, dim3(n), dim3(256), 0, s, ids, types, word, pos,
+                     type, gamma, beta, out, sents, eps);
+  return hipGetLastError();
+}
+
+hipError_t pool_normalize_packed(const f16* hidden, const PackedSentence* sents, int n, f16* out,
+                                 hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(pool_normalize_packed_kernel, dim3(n), dim3(256), 0, s, hidden, sents, out);
   return hipGetLastError();
 }
 

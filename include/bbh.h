@@ -185,6 +185,33 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
                              const int *seqs, const int64_t *emb_rows, void *emb,
                              int n_batches, bbh_stream_t stream);
 
+/* bbh_embed_packed: the embeddings bbh_embed_batches gives for the same
+ * batches when every mask is right padding (the tokenizer's layout: ones,
+ * then zeros), computed without the padding rows.  lengths (HOST array, one
+ * per sentence, batches in order) is each sentence's number of valid tokens,
+ * in [0, seqs[i]]; the mask is not read.  Only valid tokens enter the
+ * forward: the Linears and LayerNorms run over the sum of the lengths instead
+ * of sum(batch_sizes[i] * seqs[i]) rows, and attention runs per sentence over
+ * its own length (the reference pads every sentence of a batch to seq,
+ * src/model/forward.cu:20-43).  Padding rows never reach a pooled embedding
+ * (masked keys get zero weight, masked queries are left out of the mean), so
+ * each embedding is the one bbh_embed_batches computes: bit for bit while
+ * both forwards take the same LayerNorm path (a forward of more than 8192
+ * rows fuses it into the GEMM epilogue), else to within the rounding of the
+ * LayerNorm row statistics.  A sentence of length 0 gets a zero embedding.
+ * Sentences are split, in order, into one forward per pool stream of about
+ * equal token counts (more if a forward would exceed a workspace's
+ * max_batch*max_seq tokens or sentences); seqs need not be multiples of 16.
+ * Each call uploads its sentence table from pinned memory; the call orders
+ * itself after prior work on `stream`, makes later work on `stream` wait,
+ * and returns without a host sync, except that it waits for the plan copies
+ * of the call before last on this pool. */
+bbh_status bbh_embed_packed(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
+                            const int32_t *types, const int64_t *tok_offsets,
+                            const int *batch_sizes, const int *seqs, const int32_t *lengths,
+                            const int64_t *emb_rows, void *emb, int n_batches,
+                            bbh_stream_t stream);
+
 /* ---- per-launch timing of a pool ---------------------------------------------
  * HIP-event timing of each encoder op that bbh_embed_batches launches (the
  * reference times whole forwards with CUDA events, src/core/timer.h:36-39).

@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 50
+    assert len(names) == 51
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point
@@ -64,7 +64,10 @@ def test_status_strings():
 def test_workspace_bytes():
     L = _lib()
     rows = 64 * 128
-    want = sum((n + 255) // 256 * 256 for n in [rows * 1152 * 2, rows * 1536 * 2] + [rows * 384 * 2] * 4)
+    # QKV, FFN intermediate, four (rows, 384) buffers, and the packed-forward
+    # sentence table (24 bytes per possible sentence)
+    want = sum((n + 255) // 256 * 256
+               for n in [rows * 1152 * 2, rows * 1536 * 2] + [rows * 384 * 2] * 4 + [rows * 24])
     assert L.bbh_workspace_bytes(64, 128) == want
     assert L.bbh_workspace_bytes(0, 128) == 0
 

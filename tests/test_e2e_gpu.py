@@ -243,6 +243,75 @@ def test_pool_merges_equal_seq_batches(torch_cuda, ws, model, max_batch):
     assert cosine_rows(got, want).min() >= 0.99999
 
 
+def test_embed_packed_equals_padded_varlen_mix(torch_cuda, model):
+    # The whole varlen mix without its padding rows (about 27k of 93k rows)
+    # gives the padded forward's embeddings bit for bit: both forwards run
+    # over more than 8192 rows, so both fuse the LayerNorms into the GEMMs.
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    batches = synth.varlen_mix()
+    packed = engine.PackedBatches([b[:3] for b in batches])
+    assert packed.right_padded
+    assert packed.lengths.sum() < 0.5 * sum(b[0].size for b in batches)
+    pool = engine.Pool(2, 1024, 64)
+    want = _np(engine.embed_batches(pool, model, packed))
+    got = _np(engine.embed_packed(pool, model, packed))
+    torch.cuda.synchronize()
+    pool.close()
+    assert np.array_equal(got, want)
+
+
+def test_embed_packed_edge_cases(torch_cuda, model):
+    # Small forwards (both paths take the separate LayerNorm kernel): bit for
+    # bit against the padded path, with lengths 0 (zero embedding) and full,
+    # seqs that are not multiples of 32, more forwards than streams (small
+    # workspaces), and consecutive calls on one pool (the pinned plan slots
+    # alternate) with different inputs.
+    from bbh import capi, engine
+
+    torch = torch_cuda
+    rng = np.random.default_rng(5)
+
+    def batches():
+        out = []
+        for B, S in [(7, 16), (5, 48), (9, 32), (3, 80), (6, 16)]:
+            n = rng.integers(0, S + 1, size=B)
+            n[0], n[-1] = 0, S
+            mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
+            ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)
+            types = (rng.integers(0, 2, size=(B, S)) * mask).astype(np.int32)
+            out.append((ids, types, mask))
+        return out
+
+    for n_streams, max_batch in [(1, 64), (3, 2)]:
+        pool = engine.Pool(n_streams, max_batch, 80)  # (3, 2): 160-token forwards, several per stream
+        for rep in range(3):
+            packed = engine.PackedBatches(batches())
+            got = _np(engine.embed_packed(pool, model, packed))
+            want = _np(engine.embed_batches(engine.Pool(1, 16, 80), model, packed))
+            torch.cuda.synchronize()
+            assert np.array_equal(got, want), (n_streams, rep)
+            assert np.all(got[packed.lengths == 0] == 0)
+        pool.close()
+    # a length outside [0, seq] is rejected before anything is enqueued
+    packed = engine.PackedBatches(batches())
+    packed.lengths = packed.lengths.copy()
+    packed.lengths[3] = int(packed.seqs[0]) + 1
+    pool = engine.Pool(1, 64, 80)
+    with pytest.raises(capi.BBHError) as e:
+        engine.embed_packed(pool, model, packed)
+    assert e.value.name == "BBH_ERR_INVALID_ARG"
+    # masks with holes are not right padding
+    ids, types, mask = batches()[1]
+    mask = mask.copy()
+    mask[1, 0] = 0
+    mask[1, 1] = 1
+    with pytest.raises(ValueError):
+        engine.embed_packed(pool, model, engine.PackedBatches([(ids, types, mask)]))
+    pool.close()
+
+
 def test_embed_graph_replays_match_eager(torch_cuda, ws, model):
     # bert_embed captured once as a HIP graph, replayed with the inputs refilled
     # in place and eager work plus host syncs between replays: every replay

@@ -277,7 +277,7 @@ def main():
     # launch, so each event pair brackets that kernel alone.  The dominant
     # kernel is the (op, tile) class with the largest summed time per pass.
     tpool = engine.Pool(1, POOL_BATCH, 64)
-    n_ops = 6 * 5
+    n_ops = 6 * (4 + 16)  # 4 GEMMs and up to 16 attention length classes per layer
     tpool.timing(n_ops * args.steps)
     engine.embed_packed(tpool, model, packed, emb=emb_all)  # warm (records overwritten below)
     torch.cuda.synchronize()
@@ -294,15 +294,20 @@ def main():
         c["ms"] += r["ms"]
         c["n"] += 1
         c["m"].add(r["m"])
-        if r["op"] == "attention":  # packed: per sentence at its own length
-            lens = packed.lengths.astype(np.float64)
-            c["flops"] += 4.0 * r["k"] * 32 * float((lens * lens).sum())
-            c["bytes"] += float(lens.sum()) * (3 * 384 + 384) * 2.0
+        if r["op"] == "attention":
+            pass  # packed: per sentence at its own length, set below per pass
         else:
             M, N, K = r["m"], r["n"], r["k"]
             c["flops"] += 2.0 * M * N * K
             extra = M * N * 2.0 if r["op"] in ("o_proj_ln", "ffn2_ln") else 0.0  # residual
             c["bytes"] += (M * K + N * K + M * N + N) * 2.0 + extra
+    # attention launches once per 32-token length class; its work per pass is
+    # 6 layers x the sum over sentences at their own lengths
+    lens = packed.lengths.astype(np.float64)
+    for (op, tile, fused), c in classes.items():
+        if op == "attention":
+            c["flops"] = args.steps * 6 * 4.0 * 12 * 32 * float((lens * lens).sum())
+            c["bytes"] = args.steps * 6 * float(lens.sum()) * (3 * 384 + 384) * 2.0
     per_op = {}
     for (op, tile, fused), c in classes.items():
         per_op[op] = per_op.get(op, 0.0) + c["ms"] / args.steps

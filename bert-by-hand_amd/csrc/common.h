@@ -21,6 +21,7 @@ constexpr int kHeadDim = 32;
 constexpr int kFfn = 1536;
 constexpr int kVocab = 30522;
 constexpr int kMaxPos = 512;
+constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr int kTypes = 2;
 
 // Sum / max over the 64 lanes of a wavefront (butterfly, every lane gets it).

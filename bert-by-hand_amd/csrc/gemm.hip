@@ -82,8 +82,6 @@ __device__ __forceinline__ f16 to_half(float v) {
 
 enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 
-constexpr size_t kLdsMax = 160 * 1024;
-
 template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0, int SW_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SA = SA_, SW = SW_, BK = 64;
@@ -522,7 +520,10 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 // The QKV and FFN1 Linears have K = 384, so one wavefront can hold the fp16 W
 // fragments of 32 output columns for the whole K in 96 VGPRs.  A workgroup of
 // 12 wavefronts (768 threads, 3 per SIMD) then owns 384 columns and walks
-// 32-row M-tiles persistently.  Only A streams through LDS: a ring of
+// 32-row M-tiles persistently.  W arrives once, in the prologue, through LDS
+// (contiguous 1 KB copies, then fragment reads): per-lane 16-byte loads of 32
+// rows at a time ran at ~15 B/clk per CU and left ~8 us of every launch
+// before the first MFMA.  Only A streams through LDS after that: a ring of
 // wres::RING tiles of 32 x 384 (24 KB each, the 64-wide slice layout above),
 // filled with global_load_lds, two 1 KB copies per wavefront per tile.  No W
 // moves after the prologue, and each 32x32x16 MFMA reads one 1 KB A fragment
@@ -560,9 +561,38 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
   // W fragment of k-step s: row n0 + r32, k = 16 s + 8 kh .. +7 (the tiled
   // kernels' k mapping).
   f16x8 w[KS];
+  {
+    // The workgroup's 384 W rows (contiguous, 768 B each) come through LDS in
+    // three rounds of 128 rows: contiguous 1 KB global_load_lds copies, then
+    // each of the round's four wavefronts reads its 32 rows' fragments.  In
+    // LDS, 16-byte chunk c of row r sits at slot c ^ (r & 15) of the row, so
+    // the 16 rows of one fragment read fall on distinct banks.
+    constexpr int CH = K * 2 / 16;              // 48 chunks per row
+    constexpr int RR = 128;                     // rows per round
+    constexpr int CPR = RR * CH / (64 * NW);    // copies per wavefront per round (8)
+    static_assert(RR * CH % (64 * NW) == 0 && (size_t)RR * K * 2 <= LDS, "W rounds");
+    const f16* Wb = W + (size_t)ng * COLS * K;
+#pragma unroll 1
+    for (int rd = 0; rd < COLS / RR; ++rd) {
 #pragma unroll
-  for (int st = 0; st < KS; ++st)
-    w[st] = *reinterpret_cast<const f16x8*>(W + (size_t)(n0 + r32) * K + 16 * st + 8 * kh);
+      for (int j = 0; j < CPR; ++j) {
+        const int p = (j * NW + wave) * 64 + lane, row = p / CH, slot = p % CH;
+        const int chunk = slot ^ (row & 15);
+        __builtin_amdgcn_global_load_lds(
+            Wb + (size_t)(rd * RR + row) * K + chunk * 8,
+            (__attribute__((address_space(3))) void*)(smem + (j * NW + wave) * 512), 16, 0, 0);
+      }
+      wait_vm<0>();
+      lds_barrier();
+      if (wave / 4 == rd) {
+        const int row = (wave % 4) * 32 + r32;
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+          w[st] = *reinterpret_cast<const f16x8*>(smem + row * K + 8 * ((2 * st + kh) ^ (row & 15)));
+      }
+      lds_barrier();  // the next round (or the A ring) overwrites this area
+    }
+  }
   f16x4 bq[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)

@@ -135,15 +135,16 @@ __global__ __launch_bounds__(256) void embedding_ln_kernel(
 }
 
 // The packed layout: workgroup s embeds sentence s's len tokens, wavefront w
-// positions w, w + 4, ...
-__global__ __launch_bounds__(256) void embedding_ln_packed_kernel(
+// positions w, w + kPackedEmbWaves, ... (most sentences: one row per wave).
+constexpr int kPackedEmbWaves = 8;
+__global__ __launch_bounds__(64 * kPackedEmbWaves) void embedding_ln_packed_kernel(
     const int32_t* __restrict__ ids, const int32_t* __restrict__ types,
     const f16* __restrict__ word, const f16* __restrict__ pos, const f16* __restrict__ type,
     const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* __restrict__ out,
     const PackedSentence* __restrict__ sents, float eps) {
   const PackedSentence sn = sents[blockIdx.x];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int p = wave; p < sn.len; p += kRowsPerBlock)
+  for (int p = wave; p < sn.len; p += kPackedEmbWaves)
     embed_row(ids[sn.tok + p], types[sn.tok + p], p, word, pos, type, gamma, beta,
               out + (size_t)(sn.row + p) * kHidden, eps, lane);
 }
@@ -352,8 +353,8 @@ hipError_t embedding_ln_packed(const int32_t* ids, const int32_t* types, const f
                                const f16* beta, f16* out, const PackedSentence* sents, int n,
                                float eps, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(embedding_ln_packed_kernel, dim3(n), dim3(256), 0, s, ids, types, word, pos,
-                     type, gamma, beta, out, sents, eps);
+  hipLaunchKernelGGL(embedding_ln_packed_kernel, dim3(n), dim3(64 * kPackedEmbWaves), 0, s, ids,
+                     types, word, pos, type, gamma, beta, out, sents, eps);
   return hipGetLastError();
 }
 

@@ -563,34 +563,48 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
   f16x8 w[KS];
   {
     // The workgroup's 384 W rows (contiguous, 768 B each) come through LDS in
-    // three rounds of 128 rows: contiguous 1 KB global_load_lds copies, then
-    // each of the round's four wavefronts reads its 32 rows' fragments.  In
-    // LDS, 16-byte chunk c of row r sits at slot c ^ (r & 15) of the row, so
-    // the 16 rows of one fragment read fall on distinct banks.
-    constexpr int CH = K * 2 / 16;              // 48 chunks per row
-    constexpr int RR = 128;                     // rows per round
-    constexpr int CPR = RR * CH / (64 * NW);    // copies per wavefront per round (8)
-    static_assert(RR * CH % (64 * NW) == 0 && (size_t)RR * K * 2 <= LDS, "W rounds");
+    // rounds of RR rows, two LDS buffers in turn so that the copies of round
+    // r + 1 are in flight while round r is read: contiguous 1 KB
+    // global_load_lds copies, then each of the round's wavefronts reads its
+    // 32 rows' fragments.  In LDS, 16-byte chunk c of row r sits at slot
+    // c ^ (r & 15) of the row, so the 16 rows of one fragment read fall on
+    // distinct banks.
+    constexpr int CH = K * 2 / 16;            // 48 chunks per row
+    constexpr int RR = 64;                    // rows per round (32: no faster)
+    constexpr int NR = COLS / RR;             // rounds
+    constexpr int CPR = RR * CH / (64 * NW);  // copies per wavefront per round
+    constexpr int BUF = RR * K;               // halves per buffer
+    static_assert(RR * CH % (64 * NW) == 0 && (size_t)2 * BUF * 2 <= LDS && RR % 32 == 0,
+                  "W rounds");
     const f16* Wb = W + (size_t)ng * COLS * K;
-#pragma unroll 1
-    for (int rd = 0; rd < COLS / RR; ++rd) {
+    auto copy_round = [&](int rd) {
+      f16* buf = smem + (rd & 1) * BUF;
 #pragma unroll
       for (int j = 0; j < CPR; ++j) {
         const int p = (j * NW + wave) * 64 + lane, row = p / CH, slot = p % CH;
-        const int chunk = slot ^ (row & 15);
         __builtin_amdgcn_global_load_lds(
-            Wb + (size_t)(rd * RR + row) * K + chunk * 8,
-            (__attribute__((address_space(3))) void*)(smem + (j * NW + wave) * 512), 16, 0, 0);
+            Wb + (size_t)(rd * RR + row) * K + (slot ^ (row & 15)) * 8,
+            (__attribute__((address_space(3))) void*)(buf + (j * NW + wave) * 512), 16, 0, 0);
       }
-      wait_vm<0>();
+    };
+    copy_round(0);
+#pragma unroll 1
+    for (int rd = 0; rd < NR; ++rd) {
+      if (rd + 1 < NR) {
+        copy_round(rd + 1);  // its buffer was last read in round rd - 1
+        wait_vm<CPR>();      // round rd landed (copies retire in issue order)
+      } else {
+        wait_vm<0>();
+      }
       lds_barrier();
-      if (wave / 4 == rd) {
-        const int row = (wave % 4) * 32 + r32;
+      if (wave / (RR / 32) == rd) {
+        const f16* buf = smem + (rd & 1) * BUF;
+        const int row = (wave % (RR / 32)) * 32 + r32;
 #pragma unroll
         for (int st = 0; st < KS; ++st)
-          w[st] = *reinterpret_cast<const f16x8*>(smem + row * K + 8 * ((2 * st + kh) ^ (row & 15)));
+          w[st] = *reinterpret_cast<const f16x8*>(buf + row * K + 8 * ((2 * st + kh) ^ (row & 15)));
       }
-      lds_barrier();  // the next round (or the A ring) overwrites this area
+      lds_barrier();  // buffer rd & 1 is refilled by round rd + 2 (or the A ring)
     }
   }
   f16x4 bq[4];

@@ -312,6 +312,32 @@ def test_embed_packed_edge_cases(torch_cuda, model):
     pool.close()
 
 
+@pytest.mark.parametrize("S", [256, 320, 512])
+def test_embed_packed_long_sentences(torch_cuda, model, S):
+    # Long packed sentences take the other attention shapes (8 query tiles:
+    # 4 wavefronts x 2 tiles; 9-15: 8 x 1 without output staging; 16: 8 x 2),
+    # with sentences of every tile count in one launch.  Bit for bit against
+    # the padded path (both forwards under 8192 rows: separate LayerNorm).
+    from bbh import engine
+
+    torch = torch_cuda
+    rng = np.random.default_rng(S)
+    B = 16
+    n = rng.integers(0, S + 1, size=B)
+    n[:4] = [0, 1, S, 32 * (S // 64) + 1]
+    mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
+    ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)
+    types = (rng.integers(0, 2, size=(B, S)) * mask).astype(np.int32)
+    packed = engine.PackedBatches([(ids, types, mask)])
+    pool = engine.Pool(1, B, S)
+    got = _np(engine.embed_packed(pool, model, packed))
+    want = _np(engine.embed_batches(pool, model, packed))
+    torch.cuda.synchronize()
+    pool.close()
+    assert np.array_equal(got, want)
+    assert np.all(got[n == 0] == 0)
+
+
 def test_embed_graph_replays_match_eager(torch_cuda, ws, model):
     # bert_embed captured once as a HIP graph, replayed with the inputs refilled
     # in place and eager work plus host syncs between replays: every replay

@@ -539,16 +539,17 @@ constexpr int TILE = BM * K;                   // halves per A tile
 constexpr int CPW = (BM * K * 2 / 1024) / NW;  // 1 KB copies per wavefront per tile
 constexpr int COLS = NW * 32;                  // output columns per workgroup
 constexpr int kStageLd = 40;  // halves per row of a wavefront's 32 x 32 output block
-constexpr size_t LDS = ((size_t)RING * TILE + (size_t)NW * 32 * kStageLd) * sizeof(f16);
+// A ring, per-wavefront output staging, LayerNorm row partials [2][NW][32].
+constexpr size_t LDS =
+    ((size_t)RING * TILE + (size_t)NW * 32 * kStageLd) * sizeof(f16) + 2 * NW * 32 * sizeof(float);
 static_assert((BM * K * 2 / 1024) % NW == 0, "copies per wavefront");
 }  // namespace wres
 
 template <int EPI>
-__global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __restrict__ A,
-                                                                  const f16* __restrict__ W,
-                                                                  const f16* __restrict__ bias,
-                                                                  f16* __restrict__ out, int M,
-                                                                  int N) {
+__global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
+    const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
+    f16* out, int M, int N, const f16* residual = nullptr, const f16* __restrict__ gamma = nullptr,
+    const f16* __restrict__ beta = nullptr, float eps = 0.f) {
   using namespace wres;
   HIP_DYNAMIC_SHARED(f16, smem);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -607,10 +608,15 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
       lds_barrier();  // buffer rd & 1 is refilled by round rd + 2 (or the A ring)
     }
   }
+  // Bias of this lane's 16 columns, held for the whole kernel (the LayerNorm
+  // epilogue re-reads it per tile instead: its registers are spoken for).
   f16x4 bq[4];
+  auto load_bias = [&] {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    bq[j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + 8 * j + 4 * kh) : f16x4{0, 0, 0, 0};
+    for (int j = 0; j < 4; ++j)
+      bq[j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + 8 * j + 4 * kh) : f16x4{0, 0, 0, 0};
+  };
+  if (EPI != kLayerNorm) load_bias();
   const int ntiles = (M + BM - 1) / BM;
   const int my = mg < ntiles ? (ntiles - 1 - mg) / groups + 1 : 0;
   // Copy g of a tile: slice g / 4, rows (g % 4) * 8 .. +7 (copy_group's lane
@@ -658,16 +664,66 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(const f16* __r
     // acc[i] = D(n0 + 8 (i / 4) + 4 kh + i % 4, m): four 4-column runs of row m.
     const int m0 = (mg + i * groups) * BM;
     f16* stg = smem + RING * TILE + wave * 32 * kStageLd;
+    if constexpr (EPI == kLayerNorm) {
+      // N = 384: the workgroup owns whole rows.  v = acc + bias + residual,
+      // then two-pass row statistics: per-lane sums over 16 columns, lane ^ 32
+      // holds the wavefront's other 16, LDS across the 12 wavefronts.  A
+      // wavefront reads only the residual elements it then overwrites, so
+      // out may alias residual.
+      float* red = reinterpret_cast<float*>(smem + RING * TILE + NW * 32 * kStageLd);  // [2][NW][32]
+      const f16* rr = residual + (size_t)min(m0 + r32, M - 1) * N + n0 + 4 * kh;
+      load_bias();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f16x4 o;
+      for (int j = 0; j < 4; ++j) {
+        const f16x4 rv = *reinterpret_cast<const f16x4*>(rr + 8 * j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = acc[4 * j + e] + (float)bq[j][e];
-        if (EPI == kGelu) v = gelu_poly(v);
-        o[e] = to_half(v);
+        for (int e = 0; e < 4; ++e) acc[4 * j + e] += (float)bq[j][e] + (float)rv[e];
       }
-      *reinterpret_cast<f16x4*>(stg + r32 * kStageLd + 8 * j + 4 * kh) = o;
+      float sm = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sm += acc[e];
+      sm += __shfl_xor(sm, 32, kWave);
+      if (kh == 0) red[wave * 32 + r32] = sm;
+      lds_barrier();
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += red[w * 32 + r32];
+      const float mean = t * (1.0f / kHidden);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float d = acc[e] - mean;
+        q += d * d;
+      }
+      q += __shfl_xor(q, 32, kWave);
+      if (kh == 0) red[(NW + wave) * 32 + r32] = q;
+      lds_barrier();
+      float t2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t2 += red[(NW + w) * 32 + r32];
+      const float rstd = rsqrtf(t2 * (1.0f / kHidden) + eps);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f16x4 g = *reinterpret_cast<const f16x4*>(gamma + n0 + 8 * j + 4 * kh);
+        const f16x4 be = *reinterpret_cast<const f16x4*>(beta + n0 + 8 * j + 4 * kh);
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = to_half((acc[4 * j + e] - mean) * rstd * (float)g[e] + (float)be[e]);
+        *reinterpret_cast<f16x4*>(stg + r32 * kStageLd + 8 * j + 4 * kh) = o;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[4 * j + e] + (float)bq[j][e];
+          if (EPI == kGelu) v = gelu_poly(v);
+          o[e] = to_half(v);
+        }
+        *reinterpret_cast<f16x4*>(stg + r32 * kStageLd + 8 * j + 4 * kh) = o;
+      }
     }
     // Back out of this wavefront's own LDS block (no barrier needed) as
     // 16-byte stores, each instruction 16 rows x 64 contiguous bytes: 1.5-2x
@@ -692,7 +748,9 @@ bool wres_ok(int M, int N, int K) {
 
 template <int EPI>
 hipError_t launch_wres(const f16* A, const f16* W, const f16* bias, f16* out, int M, int N,
-                       hipStream_t s) {
+                       hipStream_t s, const f16* residual = nullptr, const f16* gamma = nullptr,
+                       const f16* beta = nullptr, float eps = 0.f) {
+  if (EPI == kLayerNorm && N != wres::COLS) return hipErrorInvalidValue;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_wres_kernel<EPI>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wres::LDS);
@@ -705,7 +763,7 @@ hipError_t launch_wres(const f16* A, const f16* W, const f16* bias, f16* out, in
   const int nb = N / wres::COLS, ntiles = (M + wres::BM - 1) / wres::BM;
   const int q = max(1, min(cus / (8 * nb), (ntiles + 7) / 8));
   hipLaunchKernelGGL((gemm_wres_kernel<EPI>), dim3(8 * nb * q), dim3(wres::THREADS), wres::LDS, s,
-                     A, W, bias, out, M, N);
+                     A, W, bias, out, M, N, residual, gamma, beta, eps);
   return hipGetLastError();
 }
 
@@ -894,9 +952,13 @@ int gemm_tile(int M, int N, int K) {
 // that owns whole rows leaves most CUs idle and streams all of W per
 // workgroup, so the GEMM runs on 2-D tiles with a bias + residual epilogue
 // (in place over y) and the row LayerNorm follows as its own pass.
+// The weight-resident kernel takes the K = 384 LayerNorm Linear (O-proj)
+// from M = 65536, where it passes tile 28 (89.5 vs 98.0 us at M = 131072;
+// at M = 26857 its fixed W prologue leaves it 15% behind).
 int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
   *fused_ln = M > 8192;
   if (!*fused_ln) return pick_plain(M, kHidden, K);
+  if (K == wres::K && M >= 65536) return kTiles;
   return M <= 16384 ? 14 : K >= 1024 ? 18 : 28;
 }
 
@@ -928,6 +990,8 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f
                             hipStream_t s) {
   bool fused;
   const int id = gemm_residual_ln_tile(M, K, &fused);
+  if (id == kTiles)
+    return launch_wres<kLayerNorm>(A, W, bias, y, M, kHidden, s, residual, gamma, beta, eps);
   if (fused)
     return launch_id<kLayerNorm>(id, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
   hipError_t e = launch_id<kResidual>(id, A, W, bias, residual, nullptr, nullptr, y, M, kHidden, K,
@@ -951,7 +1015,8 @@ extern "C" int bbh_tune_gemm(int id, int epi, const void* A, const void* W, cons
   auto o = static_cast<f16*>(out);
   auto st = static_cast<hipStream_t>(stream);
   if (id == kTiles) {  // the weight-resident kernel, any M
-    if (K != wres::K || N % wres::COLS != 0 || epi > 1) return hipErrorInvalidValue;
+    if (K != wres::K || N % wres::COLS != 0 || epi == 2) return hipErrorInvalidValue;
+    if (epi == 3) return launch_wres<kLayerNorm>(a, w, b, o, M, N, st, r, g, be, eps);
     return epi ? launch_wres<kGelu>(a, w, b, o, M, N, st) : launch_wres<kBias>(a, w, b, o, M, N, st);
   }
   switch (epi) {

@@ -129,7 +129,8 @@ def test_linear_reference_kat(torch_cuda, kats, tag):
 
 
 @pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384),
-                                 (12288, 384), (16384, 1536), (32768, 384), (32768, 1536)])
+                                 (12288, 384), (16384, 1536), (32768, 384), (32768, 1536),
+                                 (70001, 384)])  # the weight-resident kernel, ragged last tile
 def test_linear_residual_layernorm(torch_cuda, M, K):
     torch = torch_cuda
     from bbh import engine
@@ -147,13 +148,14 @@ def test_linear_residual_layernorm(torch_cuda, M, K):
     assert np.abs(_np(y) - want).max() <= TOL
 
 
-def test_linear_residual_layernorm_in_place(torch_cuda):
-    # y aliasing the residual is how the last layer writes the workspace's final hidden
+@pytest.mark.parametrize("M,K", [(200, 1536), (66000, 384)])
+def test_linear_residual_layernorm_in_place(torch_cuda, M, K):
+    # y aliasing the residual is how the last layer writes the workspace's
+    # final hidden (M = 66000, K = 384: the weight-resident kernel)
     torch = torch_cuda
     from bbh import engine
 
     rng = np.random.default_rng(3)
-    M, K = 200, 1536
     A, W = _h(rng, (M, K)), _h(rng, (384, K), 1.0 / np.sqrt(K))
     b, r = _h(rng, (384,), 0.1), _h(rng, (M, 384))
     g, be = np.ones(384, np.float16), np.zeros(384, np.float16)

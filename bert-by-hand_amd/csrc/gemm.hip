@@ -135,6 +135,41 @@ __device__ __forceinline__ void issue_rows(const f16* __restrict__ src, int ld, 
   }
 }
 
+// issue_rows with the per-lane part of each source address computed once:
+// off[j] = byte offset of this lane's chunk of copy j from the slice base
+// (row clamp and chunk swizzle as in issue_rows).  A K loop then pays one
+// uniform (scalar) base advance per slice instead of the per-lane address math
+// of every copy, which shares the SIMD's issue with the MFMAs.
+template <int ROWS, int NW>
+__device__ __forceinline__ void row_offsets(int ld, int valid, uint32_t (&off)[ROWS / (8 * NW)]) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < ROWS / (8 * NW); ++j) {
+    const int r = (wave * (ROWS / (8 * NW)) + j) * 8 + (lane >> 3);
+    off[j] = (uint32_t)(min(r, valid - 1) * ld + (((lane & 7) ^ Slice<64>::f(r)) << 3)) * 2u;
+  }
+}
+
+// Buffer resource over `bytes` bytes from `base` (raw, stride 0): the copy
+// unit adds a lane's 32-bit offset and a wave-uniform offset to it with no
+// vector ALU work.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// issue_rows through a buffer resource: lane chunk offsets from row_offsets,
+// slice offset `soff` bytes (wave-uniform).
+template <int ROWS, int NW>
+__device__ __forceinline__ void issue_rows_at(__amdgpu_buffer_rsrc_t src, uint32_t soff,
+                                              const uint32_t (&off)[ROWS / (8 * NW)], f16* buf) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+  for (int j = 0; j < ROWS / (8 * NW); ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        src, (__attribute__((address_space(3))) void*)(buf + (wave * (ROWS / (8 * NW)) + j) * 8 * 64),
+        16, (int)off[j], (int)soff, 0, 0);
+}
+
 // Scheduling groups: (one DS read, then ~Q/R MFMAs) x R.
 template <int R, int Q, int I = 0>
 __device__ __forceinline__ void interleave() {
@@ -191,6 +226,10 @@ __device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
   }
 }
 
+#ifndef BBH_HOIST_COPY_ADDR
+#define BBH_HOIST_COPY_ADDR 1
+#endif
+
 // The K loop.  A (activations, streamed from HBM) and W (weights, L2
 // resident) have separate LDS rings: A runs SA-1 slices ahead, W one slice
 // ahead.  Iteration j issues W(j+1) and then A(j+SA-1); because the DMA
@@ -216,12 +255,27 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
   f16* ringW = smem + C::W_BASE;
   const f16* a0 = A + (size_t)m0 * K;
   const f16* w0 = W + (size_t)n0 * K;
+#if BBH_HOIST_COPY_ADDR
+  // The launcher keeps M * K * 2 below 2^31 (row chunks), so every byte offset fits.
+  uint32_t offA[C::LA], offW[C::LW];
+  row_offsets<C::BM, C::NW>(K, M - m0, offA);
+  row_offsets<C::BN, C::NW>(K, C::BN, offW);
+  const __amdgpu_buffer_rsrc_t rA = buffer_of(a0, (uint32_t)(M - m0) * K * 2u);
+  const __amdgpu_buffer_rsrc_t rW = buffer_of(w0, (uint32_t)C::BN * K * 2u);
+  auto issueA = [&](int s) {
+    issue_rows_at<C::BM, C::NW>(rA, s * C::BK * 2, offA, ringA + (s % C::SA) * C::A_STAGE);
+  };
+  auto issueW = [&](int s) {
+    issue_rows_at<C::BN, C::NW>(rW, s * C::BK * 2, offW, ringW + (s % C::SW) * C::W_STAGE);
+  };
+#else
   auto issueA = [&](int s) {
     issue_rows<C::BM, C::NW>(a0 + s * C::BK, K, M - m0, ringA + (s % C::SA) * C::A_STAGE);
   };
   auto issueW = [&](int s) {
     issue_rows<C::BN, C::NW>(w0 + s * C::BK, K, C::BN, ringW + (s % C::SW) * C::W_STAGE);
   };
+#endif
   // Slice s of W is issued SW-1 iterations and slice s of A SA-1 iterations
   // before it is consumed; the prologue is iterations j = 1-max(SA,SW) .. -1
   // of the same schedule.
@@ -805,11 +859,21 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
         reinterpret_cast<const void*>(gemm_kernel<C, EPI>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS);
     if (attr != hipSuccess) return attr;
-    const int nb = N / C::BN, mb = (M + C::BM - 1) / C::BM;
-    const int grid = nb * 8 * ((mb + 7) / 8);
-    hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(C::THREADS), C::LDS, s, A, W, bias,
-                       residual, gamma, beta, out, M, N, K, eps);
-    return hipGetLastError();
+    // Row chunks of at most 2^30 bytes of A each: the K loop addresses A
+    // through 32-bit buffer offsets.
+    const int step = std::max(C::BM, (int)((1 << 30) / ((size_t)K * 2)) / C::BM * C::BM);
+    if ((size_t)N * K * 2 >= (1u << 31)) return hipErrorInvalidValue;
+    for (int r0 = 0; r0 < M; r0 += step) {
+      const int mr = std::min(step, M - r0);
+      const int nb = N / C::BN, mb = (mr + C::BM - 1) / C::BM;
+      const int grid = nb * 8 * ((mb + 7) / 8);
+      hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(C::THREADS), C::LDS, s,
+                         A + (size_t)r0 * K, W, bias, residual ? residual + (size_t)r0 * N : nullptr,
+                         gamma, beta, out + (size_t)r0 * N, mr, N, K, eps);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
 }
 

@@ -167,6 +167,36 @@ def test_linear_residual_layernorm_in_place(torch_cuda, M, K):
     assert np.abs(_np(rt) - want).max() <= TOL
 
 
+def test_linear_residual_layernorm_row_chunks(torch_cuda):
+    # M * K * 2 bytes of A above 2^30: the launcher splits the rows into
+    # chunks of 349440 (K = 1536), each addressed through its own 32-bit
+    # buffer range.  Rows either side of the chunk boundary and the ragged
+    # tail match the oracle, and a call over a row window that starts
+    # mid-chunk reproduces the same rows bit for bit.
+    torch = torch_cuda
+    from bbh import engine
+
+    M, K, edge = 360001, 1536, 349440
+    g = torch.Generator(device="cuda").manual_seed(11)
+    A = torch.randn((M, K), device="cuda", generator=g).half()
+    W = (torch.randn((384, K), device="cuda", generator=g) / np.sqrt(K)).half()
+    b = (torch.randn(384, device="cuda", generator=g) * 0.1).half()
+    r = torch.randn((M, 384), device="cuda", generator=g).half()
+    gm = (1 + 0.1 * torch.randn(384, device="cuda", generator=g)).half()
+    be = (0.1 * torch.randn(384, device="cuda", generator=g)).half()
+    y = torch.empty((M, 384), dtype=torch.float16, device="cuda")
+    engine.launch_linear_residual_layernorm(A, W, b, r, gm, be, y, M, K)
+    w0 = 330000  # window rows 330000 .. M-1, M = 30001: the same tile, one chunk
+    yw = torch.empty((M - w0, 384), dtype=torch.float16, device="cuda")
+    engine.launch_linear_residual_layernorm(A[w0:], W, b, r[w0:], gm, be, yw, M - w0, K)
+    torch.cuda.synchronize()
+    assert torch.equal(y[w0:], yw)
+    rows = torch.from_numpy(np.r_[0:64, edge - 64:edge + 64, M - 64:M]).cuda()
+    want = O.layer_norm(O.linear(_np(A[rows]), _np(W), _np(b)), _np(gm), _np(be),
+                        residual=_np(r[rows]))
+    assert np.abs(_np(y[rows]) - want).max() <= TOL
+
+
 # ---- LayerNorm ---------------------------------------------------------------
 
 def test_layernorm_reference_kat(torch_cuda, kats):

@@ -321,17 +321,31 @@ __device__ __forceinline__ void mainloop_reg(const f16* __restrict__ A,
   const f16* a0 = A + (size_t)m0 * K;
   const f16* w0 = W + (size_t)n0 * K;
   f16x8 ra[D][CA], rw[D][CW];
+  // Lane byte offsets of each chunk from the slice base, computed once; a
+  // slice adds its offset as the buffer instruction's scalar operand.  The
+  // launcher keeps M * K * 2 below 2^31.
+  uint32_t offA[CA], offW[CW];
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    const int c = tid + i * C::THREADS;
+    offA[i] = ((uint32_t)min(c >> 3, last) * K + (c & 7) * 8) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < CW; ++i) {
+    const int c = tid + i * C::THREADS;
+    offW[i] = ((uint32_t)(c >> 3) * K + (c & 7) * 8) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t rA = buffer_of(a0, (uint32_t)(M - m0) * K * 2u);
+  const __amdgpu_buffer_rsrc_t rW = buffer_of(w0, (uint32_t)C::BN * K * 2u);
   auto load = [&](int s, f16x8(&xa)[CA], f16x8(&xw)[CW]) {
 #pragma unroll
-    for (int i = 0; i < CA; ++i) {
-      const int c = tid + i * C::THREADS, r = c >> 3;
-      xa[i] = *reinterpret_cast<const f16x8*>(a0 + (size_t)min(r, last) * K + s * C::BK + (c & 7) * 8);
-    }
+    for (int i = 0; i < CA; ++i)
+      xa[i] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(rA, (int)offA[i], s * C::BK * 2, 0));
 #pragma unroll
-    for (int i = 0; i < CW; ++i) {
-      const int c = tid + i * C::THREADS, r = c >> 3;
-      xw[i] = *reinterpret_cast<const f16x8*>(w0 + (size_t)r * K + s * C::BK + (c & 7) * 8);
-    }
+    for (int i = 0; i < CW; ++i)
+      xw[i] = __builtin_bit_cast(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(rW, (int)offW[i], s * C::BK * 2, 0));
   };
   auto store = [&](int buf, const f16x8(&xa)[CA], const f16x8(&xw)[CW]) {
     f16* sA = smem + buf * (C::A_STAGE + C::W_STAGE);

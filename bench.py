@@ -11,6 +11,11 @@ The embeddings are those of the padded computation (bbh_embed_batches, which
 runs every padded row) bit for bit; that path is timed too and reported as
 varlen_padded_sentences_per_s.  value = sentences/s over the K timed steps.
 
+Defaults: W = 200 untimed warmup steps, K = 100 timed steps (~0.4 s of GPU
+work together).  The MI355X reaches its sustained clock only after some
+100 ms of continuous load: from a fresh process, 3 warmup steps measured
+1.50M sent/s and 200 measured 1.75M on the same box, in either order.
+
 The same line also carries, as extra fields: configs[1] (batch 64 x seq 16)
 and configs[2] (batch 64 x seq 128) sent/s (300 timed iterations as
 bench/bench.cu:32-51), configs[4] (batch 256 x seq 512) sent/s with the
@@ -156,8 +161,8 @@ def tokenizer_rate(engine, synth, n=2000, seq=128, reps=5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-extras", action="store_true", help="only the varlen workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",

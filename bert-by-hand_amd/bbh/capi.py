@@ -129,6 +129,12 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is not built; run `make -C bert-by-hand_amd` "
                                "or __graft_entry__.build()")
+        # torch first: its HIP runtime (linked as libamdhip64.so, soname
+        # libamdhip64.so.7) then also serves this library's libamdhip64.so.7
+        # dependency.  Loaded the other way round, the process ends up with
+        # two HIP runtimes and torch finds no GPU.
+        import torch  # noqa: F401
+
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

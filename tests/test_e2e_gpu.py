@@ -422,3 +422,35 @@ def test_text_to_embedding(torch_cuda, ws, model, weights32, tmp_path):
     got = _embed(torch_cuda, ws, model, ids, types, mask)
     want = O.bert_embed(weights32, ids, types, mask)
     assert cosine_rows(got, want).min() >= COS
+
+
+def test_sts_harness_matches_oracle(torch_cuda, model, weights32, tmp_path):
+    # bbh.sts end to end (bbh_tokenize -> packed embed in batches of 16 ->
+    # pair cosines -> Spearman's rho) against the fp32 oracle's embeddings of
+    # the same token ids.  Gold scores are seeded random numbers: random-init
+    # weights carry no semantics, so rho itself is only compared.  With 77
+    # pairs an adjacent rank swap moves rho by <= 12/n^2 ~ 0.002.
+    from bbh import engine, sts, synth
+
+    path = tmp_path / "vocab.txt"
+    path.write_text("\n".join(synth.text_vocab(0)) + "\n", encoding="utf-8")
+    texts = synth.texts(5, 70)[:70]
+    gold = np.random.default_rng(9).uniform(0, 5, 77)
+    rows = [(texts[i], texts[(i * 7 + 3) % 70], float(gold[i])) for i in range(70)]
+    rows += [(texts[i], texts[i], float(gold[70 + i // 10])) for i in range(0, 70, 10)]
+    sentences, pairs, scores = sts.load_corpus(rows)
+    tok = engine.Tokenizer(str(path))
+    try:
+        ids, types, mask, _ = tok(sentences, seq=64)
+        want = O.bert_embed(weights32, ids, types, mask)
+        res, emb = sts.evaluate(tok, model, rows, batch_size=16, max_seq=64)
+    finally:
+        tok.close()
+    assert res["n_sentences"] == len(sentences) == 70 and res["n_pairs"] == 77
+    assert cosine_rows(emb, want).min() >= COS
+    sims, ref = sts.pair_similarity(emb, pairs), sts.pair_similarity(want, pairs)
+    assert np.abs(sims - ref).max() <= 2e-3
+    assert sims[70:].min() >= 0.999  # identical sentences
+    assert res["spearman_rho"] == round(sts.spearman(sims, scores), 6)
+    assert abs(res["spearman_rho"] - sts.spearman(ref, scores)) <= 0.05
+    assert res["elapsed_ms"] > 0 and res["throughputs_sps"] > 0

@@ -1185,7 +1185,9 @@ bbh_status bbh_pool_timing(bbh_pool* pool, int capacity) {
   auto* t = new OpTimer;
   t->ev.assign(2 * (size_t)capacity, nullptr);
   for (auto& e : t->ev) {
-    const hipError_t err = hipEventCreate(&e);
+    // Timestamps only: without the system-scope release fence an event record
+    // is a marker, not a cache flush between the ops it brackets.
+    const hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
     if (err != hipSuccess) {
       e = nullptr;
       delete t;

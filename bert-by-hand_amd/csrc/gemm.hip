@@ -116,30 +116,15 @@ struct Cfg {
   static_assert(PD == 0 || (BM * 8 % THREADS == 0 && BN * 8 % THREADS == 0), "chunks");
 };
 
-// Copy one 64-wide K slice of ROWS K-contiguous rows into LDS.  Each
+// Copying one 64-wide K slice of ROWS K-contiguous rows into LDS: each
 // wavefront instruction fills 1 KB = 8 rows; lane i lands at row i / 8, slot
 // i % 8 of them, so it fetches the logical chunk that belongs in that slot.
-// Rows at or past `valid` are read clamped to row valid-1.
-template <int ROWS, int NW>
-__device__ __forceinline__ void issue_rows(const f16* __restrict__ src, int ld, int valid,
-                                           f16* buf) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-#pragma unroll
-  for (int j = 0; j < ROWS / (8 * NW); ++j) {
-    const int g = wave * (ROWS / (8 * NW)) + j;  // 8-row group
-    const int r = g * 8 + (lane >> 3);
-    const int cl = (lane & 7) ^ Slice<64>::f(r);
-    __builtin_amdgcn_global_load_lds(src + (size_t)min(r, valid - 1) * ld + cl * 8,
-                                     (__attribute__((address_space(3))) void*)(buf + g * 8 * 64),
-                                     16, 0, 0);
-  }
-}
-
-// issue_rows with the per-lane part of each source address computed once:
-// off[j] = byte offset of this lane's chunk of copy j from the slice base
-// (row clamp and chunk swizzle as in issue_rows).  A K loop then pays one
-// uniform (scalar) base advance per slice instead of the per-lane address math
-// of every copy, which shares the SIMD's issue with the MFMAs.
+// Rows at or past `valid` are read clamped to row valid-1.  row_offsets gives
+// off[j] = byte offset of this lane's chunk of copy j from the slice base,
+// computed once per tile; issue_rows_at then copies a slice through a buffer
+// resource, the slice's K offset being the instruction's scalar operand.  A
+// K loop so pays no per-lane address arithmetic per copy (on the SIMD issue
+// the MFMAs share: ~65 VALU instructions per wavefront per slice before).
 template <int ROWS, int NW>
 __device__ __forceinline__ void row_offsets(int ld, int valid, uint32_t (&off)[ROWS / (8 * NW)]) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -157,8 +142,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
-// issue_rows through a buffer resource: lane chunk offsets from row_offsets,
-// slice offset `soff` bytes (wave-uniform).
+// One slice's copies: lane chunk offsets from row_offsets, slice offset
+// `soff` bytes (wave-uniform).
 template <int ROWS, int NW>
 __device__ __forceinline__ void issue_rows_at(__amdgpu_buffer_rsrc_t src, uint32_t soff,
                                               const uint32_t (&off)[ROWS / (8 * NW)], f16* buf) {
@@ -226,10 +211,6 @@ __device__ __forceinline__ void compute_slice(const f16* sA, const f16* sW,
   }
 }
 
-#ifndef BBH_HOIST_COPY_ADDR
-#define BBH_HOIST_COPY_ADDR 1
-#endif
-
 // The K loop.  A (activations, streamed from HBM) and W (weights, L2
 // resident) have separate LDS rings: A runs SA-1 slices ahead, W one slice
 // ahead.  Iteration j issues W(j+1) and then A(j+SA-1); because the DMA
@@ -255,7 +236,6 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
   f16* ringW = smem + C::W_BASE;
   const f16* a0 = A + (size_t)m0 * K;
   const f16* w0 = W + (size_t)n0 * K;
-#if BBH_HOIST_COPY_ADDR
   // The launcher keeps M * K * 2 below 2^31 (row chunks), so every byte offset fits.
   uint32_t offA[C::LA], offW[C::LW];
   row_offsets<C::BM, C::NW>(K, M - m0, offA);
@@ -268,14 +248,6 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
   auto issueW = [&](int s) {
     issue_rows_at<C::BN, C::NW>(rW, s * C::BK * 2, offW, ringW + (s % C::SW) * C::W_STAGE);
   };
-#else
-  auto issueA = [&](int s) {
-    issue_rows<C::BM, C::NW>(a0 + s * C::BK, K, M - m0, ringA + (s % C::SA) * C::A_STAGE);
-  };
-  auto issueW = [&](int s) {
-    issue_rows<C::BN, C::NW>(w0 + s * C::BK, K, C::BN, ringW + (s % C::SW) * C::W_STAGE);
-  };
-#endif
   // Slice s of W is issued SW-1 iterations and slice s of A SA-1 iterations
   // before it is consumed; the prologue is iterations j = 1-max(SA,SW) .. -1
   // of the same schedule.

@@ -582,7 +582,12 @@ constexpr int kStageLd = 40;  // halves per row of a wavefront's 32 x 32 output 
 // A ring, per-wavefront output staging, LayerNorm row partials [2][NW][32].
 constexpr size_t LDS =
     ((size_t)RING * TILE + (size_t)NW * 32 * kStageLd) * sizeof(f16) + 2 * NW * 32 * sizeof(float);
-static_assert((BM * K * 2 / 1024) % NW == 0, "copies per wavefront");
+// The LayerNorm epilogue also holds the tile's residual rows ([BM][K], 16-byte
+// chunks swizzled within groups of 8) and the bias, gamma and beta of the
+// workgroup's columns.
+constexpr size_t LDS_LN = LDS + ((size_t)BM * K + 3 * (size_t)COLS) * sizeof(f16);
+static_assert(LDS_LN <= kLdsMax, "LDS");
+static_assert((BM * K * 2 / 1024) % NW == 0 && BM * K * 2 / 1024 == 2 * NW, "copies per wavefront");
 }  // namespace wres
 
 template <int EPI>
@@ -657,6 +662,20 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
       bq[j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + 8 * j + 4 * kh) : f16x4{0, 0, 0, 0};
   };
   if (EPI != kLayerNorm) load_bias();
+  // LayerNorm: bias | gamma | beta of the 384 columns once into LDS, so no
+  // global load sits in the tile loop.  The compiler's wait for a global load
+  // there is vmcnt(0), which would drain every A copy in flight each tile.
+  f16* resid = smem + RING * TILE + NW * 32 * kStageLd + 4 * NW * 32;  // after the partials
+  f16* colv = resid + BM * K;
+  if constexpr (EPI == kLayerNorm) {
+    for (int q = threadIdx.x; q < 3 * COLS / 8; q += THREADS) {
+      const int v = q / (COLS / 8), c = q % (COLS / 8);
+      const f16* src = v == 0 ? bias : v == 1 ? gamma : beta;
+      const f16x8 x = src ? *reinterpret_cast<const f16x8*>(src + ng * COLS + 8 * c)
+                          : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      *reinterpret_cast<f16x8*>(colv + v * COLS + 8 * c) = x;
+    }
+  }
   const int ntiles = (M + BM - 1) / BM;
   const int my = mg < ntiles ? (ntiles - 1 - mg) / groups + 1 : 0;
   // Copy g of a tile: slice g / 4, rows (g % 4) * 8 .. +7 (copy_group's lane
@@ -673,18 +692,42 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
           (__attribute__((address_space(3))) void*)(dst + sl * 2048 + (g & 3) * 512), 16, 0, 0);
     }
   };
+  // LayerNorm: tile i's residual rows (rows past M read row M - 1) into LDS,
+  // two 1 KB copies per wavefront; LDS chunk slot c of row r holds logical
+  // chunk (c & ~7) | ((c ^ r) & 7).
+  auto issue_res = [&](int i) {
+    const int t = mg + i * groups;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = (j * NW + wave) * 64 + lane, r = q / (K / 8), c = q % (K / 8);
+      const int cl = (c & ~7) | ((c ^ r) & 7);
+      __builtin_amdgcn_global_load_lds(
+          residual + (size_t)min(t * BM + r, M - 1) * K + cl * 8,
+          (__attribute__((address_space(3))) void*)(resid + (j * NW + wave) * 512), 16, 0, 0);
+    }
+  };
 #pragma unroll
   for (int i = 0; i < RING - 1; ++i)
     if (i < my) issue(i);
   for (int i = 0; i < my; ++i) {
-    // Tile i has landed once at most the copies of tiles i+1 .. i+RING-2 are
-    // outstanding (copies retire in issue order; the epilogue stores counted
-    // in vmcnt only make the wait stricter).
-    if (i + RING - 2 < my)
-      wait_vm<CPW * (RING - 2)>();
-    else
-      wait_vm<0>();
-    lds_barrier();  // tile i visible to all; tile i-1's slot free
+    // Tile i has landed once at most the loads issued after its copies are
+    // outstanding (loads retire in issue order among themselves; the
+    // epilogue stores, also counted in vmcnt, only make the wait stricter):
+    // the copies of tiles i+1 .. i+RING-2, and with LayerNorm also the
+    // residual copies of tiles i-2 and i-1 (issued after tile i's from i = 2).
+    if constexpr (EPI == kLayerNorm) {
+      if (i >= 2 && i + RING - 2 < my)
+        wait_vm<CPW * (RING - 2) + 4>();
+      else
+        wait_vm<0>();
+    } else {
+      if (i + RING - 2 < my)
+        wait_vm<CPW * (RING - 2)>();
+      else
+        wait_vm<0>();
+    }
+    lds_barrier();  // tile i visible to all; tile i-1's slot (and residual) free
+    if constexpr (EPI == kLayerNorm) issue_res(i);
     if (i + RING - 1 < my) issue(i + RING - 1);
     const f16* tA = smem + (i % RING) * TILE;
     f32x16 acc;
@@ -711,11 +754,21 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
       // wavefront reads only the residual elements it then overwrites, so
       // out may alias residual.
       float* red = reinterpret_cast<float*>(smem + RING * TILE + NW * 32 * kStageLd);  // [2][NW][32]
-      const f16* rr = residual + (size_t)min(m0 + r32, M - 1) * N + n0 + 4 * kh;
-      load_bias();
+      // The residual copies of this tile: only those of tile i+RING-1 were
+      // issued after them.
+      if (i + RING - 1 < my)
+        wait_vm<CPW>();
+      else
+        wait_vm<0>();
+      lds_barrier();  // every wavefront's residual copies visible
+      const f16* cv = colv + wave * 32 + 4 * kh;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const f16x4*>(cv + 8 * j);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f16x4 rv = *reinterpret_cast<const f16x4*>(rr + 8 * j);
+        const int c = wave * 4 + j;  // logical 16-byte chunk of the row: columns 8c .. 8c+7
+        const f16x4 rv = *reinterpret_cast<const f16x4*>(
+            resid + r32 * K + (((c & ~7) | ((c ^ r32) & 7)) << 3) + 4 * kh);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[4 * j + e] += (float)bq[j][e] + (float)rv[e];
       }
@@ -744,8 +797,8 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
       const float rstd = rsqrtf(t2 * (1.0f / kHidden) + eps);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f16x4 g = *reinterpret_cast<const f16x4*>(gamma + n0 + 8 * j + 4 * kh);
-        const f16x4 be = *reinterpret_cast<const f16x4*>(beta + n0 + 8 * j + 4 * kh);
+        const f16x4 g = *reinterpret_cast<const f16x4*>(cv + COLS + 8 * j);
+        const f16x4 be = *reinterpret_cast<const f16x4*>(cv + 2 * COLS + 8 * j);
         f16x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -791,9 +844,10 @@ hipError_t launch_wres(const f16* A, const f16* W, const f16* bias, f16* out, in
                        hipStream_t s, const f16* residual = nullptr, const f16* gamma = nullptr,
                        const f16* beta = nullptr, float eps = 0.f) {
   if (EPI == kLayerNorm && N != wres::COLS) return hipErrorInvalidValue;
+  constexpr size_t lds = EPI == kLayerNorm ? wres::LDS_LN : wres::LDS;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_wres_kernel<EPI>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)wres::LDS);
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -802,7 +856,7 @@ hipError_t launch_wres(const f16* A, const f16* W, const f16* bias, f16* out, in
   // One workgroup per CU: 8 XCDs x nb column blocks x q M-groups per XCD.
   const int nb = N / wres::COLS, ntiles = (M + wres::BM - 1) / wres::BM;
   const int q = max(1, min(cus / (8 * nb), (ntiles + 7) / 8));
-  hipLaunchKernelGGL((gemm_wres_kernel<EPI>), dim3(8 * nb * q), dim3(wres::THREADS), wres::LDS, s,
+  hipLaunchKernelGGL((gemm_wres_kernel<EPI>), dim3(8 * nb * q), dim3(wres::THREADS), lds, s,
                      A, W, bias, out, M, N, residual, gamma, beta, eps);
   return hipGetLastError();
 }

@@ -440,17 +440,27 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
     // The residual rows arrive through the (still free) output staging area:
     // coalesced 16-byte loads, then each lane reads its 4-column runs from
     // LDS.  Tiles staged in passes read their runs from global memory.
+    // Staged residual: global_load_lds straight into LDS (no VGPRs while the
+    // accumulators are live), unpadded [BM][384] with LDS chunk slot c of
+    // row r holding logical chunk (c & ~7) | ((c ^ r) & 7).
     constexpr bool kStageRes = C::NPASS == 1;
+    constexpr int kResCopies = C::BM * (kHidden / 8) / 64;  // 1 KB copies
+    static_assert(!kStageRes || kResCopies % C::NW == 0, "residual copies per wavefront");
+    auto res_at = [&](int r, int n) {  // halves offset of column n of staged row r
+      const int c = n >> 3;
+      return r * kHidden + (((c & ~7) | ((c ^ r) & 7)) << 3) + (n & 7);
+    };
     if constexpr (kStageRes) {
-      constexpr int CPR = kHidden / 8, PER = (C::BM * CPR + C::THREADS - 1) / C::THREADS;
 #pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        const int idx = threadIdx.x + q * C::THREADS;
-        const int r = idx / CPR, c = idx % CPR;
-        if (idx < C::BM * CPR)
-          *reinterpret_cast<f16x8*>(tile + r * C::OUT_LD + c * 8) = *reinterpret_cast<const f16x8*>(
-              residual + (size_t)min(m0 + r, M - 1) * kHidden + c * 8);
+      for (int j = 0; j < kResCopies / C::NW; ++j) {
+        const int g = j * C::NW + wave;  // 1 KB copy index
+        const int q = g * 64 + lane, r = q / (kHidden / 8), c = q % (kHidden / 8);
+        const int cl = (c & ~7) | ((c ^ r) & 7);
+        __builtin_amdgcn_global_load_lds(residual + (size_t)min(m0 + r, M - 1) * kHidden + cl * 8,
+                                         (__attribute__((address_space(3))) void*)(tile + g * 512),
+                                         16, 0, 0);
       }
+      wait_vm<0>();
       lds_barrier();
     }
 #pragma unroll
@@ -465,7 +475,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
         for (int j = 0; j < 4; ++j) {
           const int n = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
           const f16x4 rv =
-              kStageRes ? *reinterpret_cast<const f16x4*>(tile + ml * C::OUT_LD + n)
+              kStageRes ? *reinterpret_cast<const f16x4*>(tile + res_at(ml, n))
                         : *reinterpret_cast<const f16x4*>(residual + (size_t)mg * kHidden + n);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[fm][fn][4 * j + i] += (float)bvs[h][j][i] + (float)rv[i];

@@ -1,30 +1,28 @@
 """Throughput of bert_embed on one MI355X, in the driver's JSON-line format.
 
 Default workload: the synthetic varlen mix - 2000
-sentences, lognormal lengths clipped to [5, 64], consecutive batches of 64 in
-seeded order, each padded to round16(longest) (32 batches, eff 32/48/64).
-One step = one pass of bert_embed over all 32 pre-uploaded batches (the
-reference times passes over its corpus the same way, bench/corpus.cu:120-132),
-through bbh_embed_packed: only each sentence's valid tokens enter the forward
-(26,857 of the 91,648 padded rows), as one forward on N_STREAMS stream(s).
-The embeddings are those of the padded computation (bbh_embed_batches, which
-runs every padded row) bit for bit; that path is timed too and reported as
-varlen_padded_sentences_per_s.  value = sentences/s over the K timed steps.
+sentences, lognormal lengths clipped to [5, 64], 32 consecutive batches of 64
+in seeded order, each padded to round16(longest) (eff 32/48/64, 91,648 padded
+rows).  One step = one bert_embed per batch at its padded length, as the
+reference's corpus benchmark loops over its batches (bench/corpus.cu:120-132):
+bbh_embed_each runs each batch as its own forward (nothing merged, every
+padding row computed) and spreads the 32 forwards over EACH_STREAMS
+concurrent HIP streams, one workspace each.  value = sentences/s over the K
+timed steps, inputs pre-uploaded to HBM.
 
-Defaults: W = 200 untimed warmup steps, K = 100 timed steps (~0.4 s of GPU
-work together).  The MI355X reaches its sustained clock only after some
-100 ms of continuous load: from a fresh process, 3 warmup steps measured
-1.50M sent/s and 200 measured 1.75M on the same box, in either order.
+The roofline names the dominant kernel class of that pass: the same pass on a
+one-stream pool with a pair of HIP events around every launch on that stream
+(so no other stream shares the GPU during a launch); achieved = algorithmic
+FLOPs (GEMMs, attention) or bytes (row kernels) per launch / mean launch time.
 
-The same line also carries, as extra fields: configs[1] (batch 64 x seq 16)
-and configs[2] (batch 64 x seq 128) sent/s (300 timed iterations as
-bench/bench.cu:32-51), configs[4] (batch 256 x seq 512) sent/s with the
-fused GEMMs' fraction of the fp16 dense MFMA peak, the roofline of the
-dominant kernel of the default workload (the same packed runs through a
-one-stream pool, timed live with an event pair around each launch on that
-stream, so no other stream's kernels share the GPU during a launch), and the
-CPU baseline (the fp32 numpy oracle on a bounded sample, on this host's
-cores).
+Extra fields: the same pass on one stream; the reference corpus benchmark's
+two modes on the same sentences (length-sorted dynamic batches, and every
+batch at seq 128, bench/corpus.cu:64-132); the padding-free packed pass and
+the equal-seq-merged padded pass; configs[1] / configs[2] (batch 64 x seq
+16 / 128, 300 iterations as bench/bench.cu:32-51); configs[4] (batch 256 x
+seq 512) with the fused GEMMs' fraction of the fp16 dense MFMA peak; the
+tokenizer rate; and the CPU baseline (transformers' BertModel fp32 forward, the
+library the reference's cpu_fp32 leg times, on this host's cores).
 """
 
 import argparse
@@ -40,10 +38,12 @@ for _p in (ROOT, os.path.join(ROOT, "bert-by-hand_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-N_STREAMS = 1  # forwards of the packed varlen pass (one workspace per stream)
-PAD_STREAMS = 2  # concurrent forwards of the padded varlen pass
-POOL_BATCH = 1024  # workspace rows per stream = POOL_BATCH * 64: the 21 batches of
-#                    padded length 48 (64,512 rows) run as one padded forward
+EACH_STREAMS = 3  # concurrent per-batch forwards.  HIP maps streams onto GPU_MAX_HW_QUEUES = 4
+#                  hardware queues and the caller's stream holds one, so 3 pool streams get
+#                  a queue each (measured per pass: 1 stream 10.5 ms, 2 6.6, 3 5.4, 4 6.2-7.0
+#                  (two streams share a queue), 6 5.4-5.8; with 5-8 hardware queues every
+#                  configuration above 3 busy queues took 11-22 ms)
+POOL_BATCH = 1024  # workspace rows of the packed / merged pool = POOL_BATCH * 64
 PEAK_FP16_DENSE = 2.5e15  # MI355X published dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
 EPI_OF_OP = {"qkv": "0 (bias)", "ffn1_gelu": "1 (bias+GELU)"}
@@ -98,30 +98,52 @@ def gemm_buffers(torch, max_m):
                 be=torch.zeros(384, dtype=torch.float16, device="cuda"))
 
 
-def cpu_baseline(batches, weights, budget_s=12.0):
-    """The fp32 numpy oracle (the reference's fp32 torch forward restated) on
-    the first batches of the same workload, until ~budget_s of CPU work."""
-    from oracle import bert_oracle as O
-
+def cpu_model():
     try:
-        from threadpoolctl import threadpool_info
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:  # pragma: no cover
+        pass
+    import platform
 
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    O.bert_embed(weights, *batches[0][:3])  # warm
-    n_sent, t0, used = 0, time.perf_counter(), 0
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(batches, weights, budget_s=15.0):
+    """The reference's torch CPU fp32 forward (transformers BertModel + mean
+    pool + L2 normalize, the library its cpu_fp32 leg times,
+    scripts/benchmark.py:64-86,110-111) on the same varlen batches and seeded
+    weights, on this host's cores: 3 warmup forwards, then consecutive batches
+    until ~budget_s of CPU work."""
+    import torch
+
+    from oracle import torch_forward as T
+
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(os.cpu_count() or 1, avail or 1, omp or (os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    model = T.build(weights)
+    for _ in range(3):
+        T.embed(model, *batches[0][:3])
+    n_sent, used, t0 = 0, 0, time.perf_counter()
     for ids, types, mask, _ in batches:
-        O.bert_embed(weights, ids, types, mask)
+        T.embed(model, ids, types, mask)
         n_sent += ids.shape[0]
         used += 1
         if time.perf_counter() - t0 > budget_s:
             break
     dt = time.perf_counter() - t0
-    return {"value": round(n_sent / dt, 1), "unit": "sentences/s", "cores": int(cores),
+    return {"value": round(n_sent / dt, 1), "unit": "sentences/s", "cores": int(torch.get_num_threads()),
             "kind": "port",
-            "sample": f"fp32 numpy oracle bert_embed over the first {used} batches "
-                      f"({n_sent} sentences) of the varlen mix, {dt:.1f} s"}
+            "sample": f"transformers BertModel fp32 (sdpa) + mean pool + L2 normalize, torch "
+                      f"{torch.__version__}, one forward per batch over the first {used} of the 32 "
+                      f"varlen batches ({n_sent} sentences, padded as on the GPU), {dt:.1f} s after 3 "
+                      f"warmup forwards",
+            "ms_per_sentence": round(dt / n_sent * 1e3, 4),
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "affinity_cpus": avail,
+            "omp_num_threads": omp or None}
 
 
 def tokenizer_rate(engine, synth, n=2000, seq=128, reps=5):
@@ -158,11 +180,88 @@ def tokenizer_rate(engine, synth, n=2000, seq=128, reps=5):
     return out
 
 
+def pass_timer(torch, fn, steps, warmup):
+    """(ms per pass between events on the current stream, wall ms per pass)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps, (time.perf_counter() - t0) / steps * 1e3
+
+
+def launch_work(r):
+    """Algorithmic (FLOPs, HBM bytes) of one recorded launch (bbh_launch_time)."""
+    op, M, N, K = r["op"], r["m"], r["n"], r["k"]
+    if op == "attention":  # (batch, seq, heads); padded keys count (the kernel visits them)
+        B, S, H = M, N, K
+        return 4.0 * B * H * 32 * S * S, B * S * (3 * 384 + 384) * 2.0 + 4.0 * B * S
+    if op == "embed":  # rows: ids + types + word row in, hidden row out; pos/type rows from L2
+        return 0.0, M * (8.0 + 768 + 768)
+    if op == "pool":  # (batch, seq): hidden + mask in, embedding out
+        return 0.0, M * N * (768.0 + 4) + M * 768.0
+    if op == "layernorm":  # rows read and written in place, gamma/beta
+        return 0.0, M * 1536.0 + 1536
+    flops = 2.0 * M * N * K
+    byts = (M * K + N * K + M * N + N) * 2.0
+    if op in ("o_proj_ln", "ffn2_ln"):
+        byts += M * N * 2.0  # the residual
+    return flops, byts
+
+
+def kernel_name(engine, op, tile, fused):
+    if op == "attention":
+        return "attention_kernel"
+    if op == "embed":
+        return "embedding_ln_kernel"
+    if op == "pool":
+        return "pool_normalize_kernel"
+    if op == "layernorm":
+        return "ln384_kernel"
+    epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else "2 (bias+residual)")
+    tname = engine.gemm_tile_name(tile)
+    return (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
+            f"gemm_kernel<{tname}, {epi}>")
+
+
+def classify(engine, recs, steps):
+    """Launch records -> classes keyed (op, tile, fused): summed ms, count, M
+    values, algorithmic FLOPs and bytes."""
+    classes = {}
+    for r in recs:
+        key = (r["op"], r["tile"], r["fused_ln"])
+        c = classes.setdefault(key, {"ms": 0.0, "n": 0, "flops": 0.0, "bytes": 0.0, "m": set()})
+        f, b = launch_work(r)
+        c["ms"] += r["ms"]
+        c["n"] += 1
+        c["m"].add(r["m"])
+        c["flops"] += f
+        c["bytes"] += b
+    total = sum(c["ms"] for c in classes.values())
+    rows = []
+    for (op, tile, fused), c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
+        avg_s = c["ms"] / c["n"] / 1e3
+        rows.append({"kernel": kernel_name(engine, op, tile, fused), "op": op, "m": sorted(c["m"]),
+                     "launches_per_step": round(c["n"] / steps, 2),
+                     "avg_launch_us": round(avg_s * 1e6, 2),
+                     "tflops": round(c["flops"] / c["n"] / avg_s / 1e12, 1),
+                     "gb_per_s": round(c["bytes"] / c["n"] / avg_s / 1e9, 1),
+                     "algorithmic_flops_per_launch": round(c["flops"] / c["n"]),
+                     "algorithmic_bytes_per_launch": round(c["bytes"] / c["n"]),
+                     "share_of_op_time": round(c["ms"] / total, 3)})
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-extras", action="store_true", help="only the varlen workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -193,62 +292,31 @@ def main():
         return
     weights = synth.make_weights(0)
     model = engine.Model.from_weights(weights)
-    ws = engine.Workspace(256, 512)
 
-    # ---- default workload: varlen mix ------------------------------------
-    # All 32 batches pre-uploaded; bert_embed on every batch through
-    # bbh_embed_packed (valid tokens only) on a pool of N_STREAMS streams.
+    # ---- default workload: varlen mix, one bert_embed per batch ------------
+    # The 32 consecutive batches of 64, each at its own padded round16 length,
+    # pre-uploaded back to back; one step = bert_embed on every batch
+    # (bbh_embed_each: one forward per batch, nothing merged, every padding
+    # row computed), the batches spread over EACH_STREAMS pool streams.
     batches = synth.varlen_mix()
     n_sent = sum(b[0].shape[0] for b in batches)
-    packed = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
-    real_tokens = int(packed.lengths.sum())
     padded_rows = int(sum(b[0].size for b in batches))
-    pool = engine.Pool(N_STREAMS, POOL_BATCH, 64)
-    emb_all = torch.empty((packed.rows, 384), dtype=torch.float16, device="cuda")
-
-    def step():
-        engine.embed_packed(pool, model, packed, emb=emb_all)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    s_ev.record()
-    for _ in range(args.steps):
-        step()
-    e_ev.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = s_ev.elapsed_time(e_ev) / args.steps
+    pk = engine.PackedBatches([b[:3] for b in batches])  # consecutive order, as given
+    real_tokens = int(pk.lengths.sum())
+    emb_all = torch.empty((pk.rows, 384), dtype=torch.float16, device="cuda")
+    pool = engine.Pool(EACH_STREAMS, 64, 64)
+    ms_step, wall = pass_timer(torch, lambda: engine.embed_each(pool, model, pk, emb=emb_all),
+                               args.steps, args.warmup)
     sps = n_sent / (ms_step / 1e3)
-    # algorithmic FLOPs over the valid tokens (what the packed pass executes)
-    total_flops = sum(synth.flops_per_forward(1, int(L)) for L in packed.lengths)
-    log(f"varlen packed ({N_STREAMS} stream(s), {real_tokens} of {padded_rows} rows): "
-        f"{ms_step:.3f} ms/pass ({wall / args.steps * 1e3:.3f} ms wall), {sps:,.0f} sent/s, "
-        f"{total_flops / (ms_step / 1e3) / 1e12:.1f} TFLOP/s executed")
-
-    # the padded computation (every padded row) through bbh_embed_batches
-    ppool = engine.Pool(PAD_STREAMS, POOL_BATCH, 64)
-    ms_pad = timed(torch, lambda: engine.embed_batches(ppool, model, packed, emb=emb_all),
-                   args.steps, warmup=args.warmup)
-    ppool.close()
     pad_flops = sum(synth.flops_per_forward(b[0].shape[0], b[3]) for b in batches)
-    log(f"varlen padded ({PAD_STREAMS} streams, {padded_rows} rows): {ms_pad:.3f} ms/pass, "
-        f"{n_sent / (ms_pad / 1e3):,.0f} sent/s, "
-        f"{pad_flops / (ms_pad / 1e3) / 1e12:.1f} TFLOP/s executed")
+    log(f"varlen per-batch bert_embed ({EACH_STREAMS} streams, {padded_rows} padded rows): "
+        f"{ms_step:.3f} ms/pass ({wall:.3f} ms wall), {sps:,.0f} sent/s, "
+        f"{pad_flops / (ms_step / 1e3) / 1e12:.1f} TFLOP/s executed")
 
-    # the same workload as one bert_embed per batch on a single stream
-    dev = [(torch.from_numpy(i).cuda(), torch.from_numpy(t).cuda(), torch.from_numpy(m).cuda())
-           for i, t, m, _ in batches]
-    emb = torch.empty((64, 384), dtype=torch.float16, device="cuda")
-
-    def step1():
-        for i, t, m in dev:
-            engine.bert_embed(ws, model, i, t, m, emb=emb[: i.shape[0]])
-
-    ms1 = timed(torch, step1, args.steps, warmup=args.warmup)
-    log(f"varlen (1 stream): {ms1:.3f} ms/pass, {n_sent / (ms1 / 1e3):,.0f} sent/s")
+    pool1 = engine.Pool(1, 64, 64)
+    ms1, _ = pass_timer(torch, lambda: engine.embed_each(pool1, model, pk, emb=emb_all),
+                        args.steps, args.warmup // 2)
+    log(f"varlen per-batch bert_embed (1 stream): {ms1:.3f} ms/pass, {n_sent / (ms1 / 1e3):,.0f} sent/s")
 
     out = {
         "metric": "sentences/sec (batch 64, seq 16/128 + varlen mix); % of MFMA fp16 peak",
@@ -256,121 +324,116 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded random-init MiniLM-L6 weights N(0,0.02), synthetic token ids)",
-        "config": {"workload": "varlen mix: 2000 sentences, lognormal(median 12, sigma 0.5) "
-                               "lengths clipped to [5,64], consecutive batches of 64 padded to "
-                               f"round16(max) ({padded_rows} padded rows, {real_tokens} valid "
-                               "tokens); one step = bert_embed over all 32 batches via "
-                               "bbh_embed_packed: only valid tokens enter the forward (one "
-                               f"forward of {real_tokens} rows on {N_STREAMS} stream(s)); the "
-                               "embeddings equal the padded computation's (bbh_embed_batches) "
-                               "bit for bit",
-                   "streams": N_STREAMS, "pool_rows_per_stream": POOL_BATCH * 64,
+        "config": {"workload": "varlen mix (BASELINE configs[3]): 2000 sentences, "
+                               "lognormal(median 12, sigma 0.5) lengths clipped to [5,64], 32 "
+                               "consecutive batches of 64 in seeded order, each padded to "
+                               f"round16(max) (eff 32/48/64, {padded_rows} padded rows, "
+                               f"{real_tokens} valid tokens); one step = one bert_embed per "
+                               "batch at its padded length (bbh_embed_each: nothing merged, "
+                               "every padding row computed), the 32 forwards spread over "
+                               f"{EACH_STREAMS} concurrent HIP streams with one workspace each",
+                   "streams": EACH_STREAMS,
                    "model": "MiniLM-L6 (6 layers, hidden 384, 12x32 heads, FFN 1536)",
                    "global_batch": 64,
                    "seq_len": f"5..64 valid ({real_tokens / n_sent:.1f} mean), padded 32/48/64",
                    "parallelism": "single GPU"},
         "ms_per_sentence": round(ms_step / n_sent, 6),
-        "varlen_padded_sentences_per_s": round(n_sent / (ms_pad / 1e3), 1),
-        "varlen_padded_streams": PAD_STREAMS,
-        "varlen_single_stream_sentences_per_s": round(n_sent / (ms1 / 1e3), 1),
-        "executed_tflops": round(total_flops / (ms_step / 1e3) / 1e12, 2),
+        "executed_tflops": round(pad_flops / (ms_step / 1e3) / 1e12, 2),
+        "varlen_per_batch_1stream_sentences_per_s": round(n_sent / (ms1 / 1e3), 1),
+        "varlen_per_batch_1stream_ms_per_pass": round(ms1, 4),
     }
 
     # ---- dominant kernel of the default workload ---------------------------
-    # The same packed pass again, through a one-stream pool with per-launch
-    # timing on: a pair of HIP events on the pool stream around every op
-    # launch, so each event pair brackets that kernel alone.  The dominant
-    # kernel is the (op, tile) class with the largest summed time per pass.
-    tpool = engine.Pool(1, POOL_BATCH, 64)
-    n_ops = 6 * (4 + 16)  # 4 GEMMs and up to 16 attention length classes per layer
-    tpool.timing(n_ops * args.steps)
-    engine.embed_packed(tpool, model, packed, emb=emb_all)  # warm (records overwritten below)
+    # The same per-batch pass on a one-stream pool with per-launch timing: a
+    # pair of HIP events on the pool stream around every op launch, so each
+    # pair brackets that kernel alone with no other stream sharing the GPU.
+    n_ops = 32 * (2 + 6 * 7)
+    pool1.timing(n_ops)
+    engine.embed_each(pool1, model, pk, emb=emb_all)  # warm (records overwritten below)
     torch.cuda.synchronize()
-    tpool.timing(n_ops * args.steps)
-    for _ in range(args.steps):
-        engine.embed_packed(tpool, model, packed, emb=emb_all)
-    recs = tpool.timing_read()
-    tpool.timing(0)
-    tpool.close()
-    classes = {}
-    for r in recs:
-        key = (r["op"], r["tile"], r["fused_ln"])
-        c = classes.setdefault(key, {"ms": 0.0, "n": 0, "flops": 0.0, "bytes": 0.0, "m": set()})
-        c["ms"] += r["ms"]
-        c["n"] += 1
-        c["m"].add(r["m"])
-        if r["op"] == "attention":
-            pass  # packed: per sentence at its own length, set below per pass
-        else:
-            M, N, K = r["m"], r["n"], r["k"]
-            c["flops"] += 2.0 * M * N * K
-            extra = M * N * 2.0 if r["op"] in ("o_proj_ln", "ffn2_ln") else 0.0  # residual
-            c["bytes"] += (M * K + N * K + M * N + N) * 2.0 + extra
-    # attention launches once per 32-token length class; its work per pass is
-    # 6 layers x the sum over sentences at their own lengths
-    lens = packed.lengths.astype(np.float64)
-    for (op, tile, fused), c in classes.items():
-        if op == "attention":
-            c["flops"] = args.steps * 6 * 4.0 * 12 * 32 * float((lens * lens).sum())
-            c["bytes"] = args.steps * 6 * float(lens.sum()) * (3 * 384 + 384) * 2.0
-    per_op = {}
-    for (op, tile, fused), c in classes.items():
-        per_op[op] = per_op.get(op, 0.0) + c["ms"] / args.steps
-
-    def kernel_name(op, tile, fused):
-        if op == "attention":
-            return "attention_kernel"
-        epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else
-                                    "2 (bias+residual), then ln384_kernel")
-        tname = engine.gemm_tile_name(tile)
-        return (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
-                f"gemm_kernel<{tname}, {epi}>")
-
-    key = max(classes, key=lambda k: classes[k]["ms"])
-    op, tile, fused = key
-    c = classes[key]
-    avg_s = c["ms"] / c["n"] / 1e3
-    ach = c["flops"] / c["n"] / avg_s
-    kname = kernel_name(op, tile, fused)
-    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE summary
-    # (one entry per leading kernel class of the profiled run)
+    tsteps = max(5, args.steps // 5)
+    pool1.timing(n_ops * tsteps)
+    for _ in range(tsteps):
+        engine.embed_each(pool1, model, pk, emb=emb_all)
+    recs = pool1.timing_read()
+    pool1.timing(0)
+    classes = classify(engine, recs, tsteps)
+    dom = classes[0]
+    gemm = not dom["op"] in ("embed", "pool", "layernorm")
+    ach = dom["tflops"] if gemm else dom["gb_per_s"]
+    peak = PEAK_FP16_DENSE / 1e12 if gemm else PEAK_HBM / 1e9
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
     if os.path.exists(tfile):
         for t in json.load(open(tfile)).get("kernels", []):
-            if t.get("kernel") == kname and t.get("op") == op and t.get("m") == sorted(c["m"]):
+            if t.get("kernel") == dom["kernel"] and t.get("op") == dom["op"] and t.get("m") == dom["m"]:
                 traffic = t["traffic_bytes_per_launch"]
     out["roofline"] = {
-        "bound": "mfma", "achieved": round(ach / 1e12, 2), "peak": PEAK_FP16_DENSE / 1e12,
-        "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_DENSE, 4), "traffic": traffic,
-        "kernel": kname, "op": op, "m": sorted(c["m"]),
-        "launches_per_step": c["n"] // args.steps,
-        "avg_launch_us": round(avg_s * 1e6, 2),
-        "algorithmic_flops_per_launch": round(c["flops"] / c["n"]),
-        "algorithmic_bytes_per_launch": round(c["bytes"] / c["n"]),
-        "share_of_op_time": round(c["ms"] / sum(v["ms"] for v in classes.values()), 3)}
-    out["op_ms_per_step"] = {k: round(v, 4) for k, v in sorted(per_op.items())}
-
-    top = sorted(classes, key=lambda k: -classes[k]["ms"])[:3]
-    out["top_kernel_classes"] = [
-        {"kernel": kernel_name(*k), "op": k[0], "m": sorted(classes[k]["m"]),
-         "avg_launch_us": round(classes[k]["ms"] / classes[k]["n"] * 1e3, 2),
-         "algorithmic_bytes_per_launch": round(classes[k]["bytes"] / classes[k]["n"]),
-         "share_of_op_time": round(classes[k]["ms"] / sum(v["ms"] for v in classes.values()), 3)}
-        for k in top]
-    by_m = {}
-    for r in recs:
-        d = by_m.setdefault(r["op"], {}).setdefault(r["m"], [0.0, 0])
-        d[0] += r["ms"]
-        d[1] += 1
-    out["op_us_per_launch_by_m"] = {op: {m: round(t / n * 1e3, 2) for m, (t, n) in sorted(d.items())}
-                                    for op, d in sorted(by_m.items())}
+        "bound": "mfma" if gemm else "hbm", "achieved": ach, "peak": peak,
+        "unit": "TFLOP/s" if gemm else "GB/s", "frac": round(ach / peak, 4), "traffic": traffic,
+        "kernel": dom["kernel"], "op": dom["op"], "m": dom["m"],
+        "launches_per_step": dom["launches_per_step"], "avg_launch_us": dom["avg_launch_us"],
+        "algorithmic_flops_per_launch": dom["algorithmic_flops_per_launch"],
+        "algorithmic_bytes_per_launch": dom["algorithmic_bytes_per_launch"],
+        "share_of_op_time": dom["share_of_op_time"],
+        "timing": f"one-stream pool, event pair per launch, {tsteps} passes"}
+    out["kernel_classes"] = classes[:12]
     log("roofline", out["roofline"])
-    log("op ms per step", out["op_ms_per_step"])
-    log("op us per launch by M", out["op_us_per_launch_by_m"])
+    for c in classes[:12]:
+        log("  ", c)
 
-    buf = gemm_buffers(torch, 131072)
     if not args.no_extras:
+        # ---- the reference corpus benchmark's two modes on the same sentences
+        sb, order = synth.varlen_sorted()
+        pb = synth.varlen_padded()
+        for tag, bl, desc in (
+                ("corpus_sorted_dynamic", sb, "sentences stable-sorted by length, batches of 64 "
+                 "at max(16, round16(longest)) (bench/corpus.cu:79-132)"),
+                ("corpus_padded_128", pb, "consecutive batches of 64 at seq 128 "
+                 "(bench/corpus.cu:64-77)")):
+            pkc = engine.PackedBatches([b[:3] for b in bl])
+            if tag == "corpus_padded_128":
+                cp = engine.Pool(EACH_STREAMS, 64, 128)
+                cp1 = engine.Pool(1, 64, 128)
+            else:
+                cp, cp1 = pool, pool1
+            msc, _ = pass_timer(torch, lambda: engine.embed_each(cp, model, pkc, emb=emb_all),
+                                args.steps, args.warmup // 2)
+            msc1, _ = pass_timer(torch, lambda: engine.embed_each(cp1, model, pkc, emb=emb_all),
+                                 max(10, args.steps // 2), 10)
+            fl = sum(synth.flops_per_forward(b[0].shape[0], b[3]) for b in bl)
+            out[tag] = {"sentences_per_s": round(n_sent / (msc / 1e3), 1), "streams": EACH_STREAMS,
+                        "ms_per_pass": round(msc, 4),
+                        "sentences_per_s_1stream": round(n_sent / (msc1 / 1e3), 1),
+                        "padded_rows": int(sum(b[0].size for b in bl)),
+                        "executed_tflops": round(fl / (msc / 1e3) / 1e12, 2), "batching": desc}
+            if cp is not pool:
+                cp.close()
+                cp1.close()
+            log(tag, out[tag])
+
+        # ---- the same sentences without padding, and with equal-seq batches merged
+        pkg = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
+        ppool = engine.Pool(1, POOL_BATCH, 64)
+        ms_p, _ = pass_timer(torch, lambda: engine.embed_packed(ppool, model, pkg, emb=emb_all),
+                             args.steps, args.warmup)
+        ms_m, _ = pass_timer(torch, lambda: engine.embed_batches(ppool, model, pkg, emb=emb_all),
+                             args.steps, args.warmup // 2)
+        ppool.close()
+        valid_flops = sum(synth.flops_per_forward(1, int(L)) for L in pkg.lengths)
+        out["varlen_packed"] = {
+            "sentences_per_s": round(n_sent / (ms_p / 1e3), 1), "ms_per_pass": round(ms_p, 4),
+            "executed_tflops": round(valid_flops / (ms_p / 1e3) / 1e12, 2),
+            "what": f"bbh_embed_packed: only the {real_tokens} valid tokens enter one forward "
+                    "(no padding rows), same embeddings as the padded batches"}
+        out["varlen_merged_padded"] = {
+            "sentences_per_s": round(n_sent / (ms_m / 1e3), 1), "ms_per_pass": round(ms_m, 4),
+            "what": "bbh_embed_batches: runs of equal-seq batches merged into one forward per "
+                    "run (one stream), every padding row computed"}
+        log("packed", out["varlen_packed"], "merged", out["varlen_merged_padded"])
+
+        ws = engine.Workspace(256, 512)
+        emb = torch.empty((64, 384), dtype=torch.float16, device="cuda")
         # ---- batch 64 x seq 16 / 128 ----------------
         for tag, seq in (("cfg2_b64_s16", 16), ("cfg3_b64_s128", 128)):
             ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(64, seq))
@@ -387,6 +450,7 @@ def main():
                         "graph_ms_per_sentence": round(ms_g / 64, 6)}
             log(tag, out[tag])
         # ---- batch 256 x seq 512 ---------------------------------
+        buf = gemm_buffers(torch, 131072)
         ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())
         emb5 = torch.empty((256, 384), dtype=torch.float16, device="cuda")
         ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb5), 10,
@@ -400,6 +464,7 @@ def main():
             gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
             gemm_ms += t
             gemm_flops += f
+        del buf
         # the same batch through bbh_embed_packed (valid tokens only: lengths
         # uniform in [256, 512], so about 3/4 of the padded rows)
         pk5 = engine.PackedBatches([synth.long_batch()])
@@ -407,6 +472,7 @@ def main():
         ms_p5 = timed(torch, lambda: engine.embed_packed(pool5, model, pk5, emb=emb5), 10,
                       warmup=2)
         pool5.close()
+        ws.close()
         out["cfg5_b256_s512"] = {
             "sentences_per_s": round(256 / (ms / 1e3), 1), "ms_per_forward": round(ms, 3),
             "packed_sentences_per_s": round(256 / (ms_p5 / 1e3), 1),
@@ -415,8 +481,6 @@ def main():
             "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
             "per_gemm_frac": gem}
         log("cfg5", out["cfg5_b256_s512"])
-
-    if not args.no_extras:
         out["tokenizer"] = tokenizer_rate(engine, synth)
         log("tokenizer", out["tokenizer"])
 
@@ -427,7 +491,7 @@ def main():
         out["cpu_baseline"] = None
 
     pool.close()
-    ws.close()
+    pool1.close()
     model.close()
     print(json.dumps(out), flush=True)
 

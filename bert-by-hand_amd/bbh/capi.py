@@ -63,6 +63,8 @@ SIGNATURES = {
     "bbh_pool_free": (c_int, [c_void_p]),
     "bbh_embed_batches": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "bbh_embed_each": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                               c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "bbh_embed_packed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "bbh_pool_timing": (c_int, [c_void_p, c_int]),

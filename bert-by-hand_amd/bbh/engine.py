@@ -170,7 +170,8 @@ class Pool:
         """Start timing each op of later embed_batches calls (0 stops)."""
         call("bbh_pool_timing", self.handle, capacity)
 
-    OPS = {1: "qkv", 2: "attention", 3: "o_proj_ln", 4: "ffn1_gelu", 5: "ffn2_ln"}
+    OPS = {1: "qkv", 2: "attention", 3: "o_proj_ln", 4: "ffn1_gelu", 5: "ffn2_ln", 6: "embed",
+           7: "pool", 8: "layernorm"}
 
     def timing_read(self):
         """The recorded launches: dicts of op, tile, fused_ln, m, n, k, ms."""
@@ -252,6 +253,20 @@ def embed_batches(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=
         emb = torch.empty((packed.rows, HIDDEN), dtype=torch.float16, device="cuda")
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
     call("bbh_embed_batches", pool.handle, w.handle, _ptr(packed.ids), _ptr(packed.types),
+         _ptr(packed.mask), p(packed.tok_offsets), p(packed.sizes), p(packed.seqs),
+         p(packed.emb_rows), _ptr(emb), packed.n, _stream(stream))
+    return emb
+
+
+def embed_each(pool: Pool, w: Model, packed: PackedBatches, emb=None, stream=None):
+    """One bert_embed per packed batch (the reference's corpus loop,
+    bench/corpus.cu:120-132), the batches spread over the pool's streams;
+    nothing is merged (bbh_embed_each).  (rows, 384) fp16, in batch order."""
+    torch = _torch()
+    if emb is None:
+        emb = torch.empty((packed.rows, HIDDEN), dtype=torch.float16, device="cuda")
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    call("bbh_embed_each", pool.handle, w.handle, _ptr(packed.ids), _ptr(packed.types),
          _ptr(packed.mask), p(packed.tok_offsets), p(packed.sizes), p(packed.seqs),
          p(packed.emb_rows), _ptr(emb), packed.n, _stream(stream))
     return emb

@@ -149,19 +149,45 @@ def varlen_lengths(n: int = 2000, seed: int = 0) -> np.ndarray:
     return np.clip(np.round(rng.lognormal(np.log(12), 0.5, n)), 5, 64).astype(np.int64)
 
 
+def varlen_rows(n: int = 2000, seed: int = 0) -> list:
+    """The sentences of configs[3], in seeded order."""
+    lengths = varlen_lengths(n, seed)
+    rng = np.random.default_rng(seed + 1)
+    return [sentence(rng, int(L)) for L in lengths]
+
+
+def batches_of(rows, batch: int = 64, seq=None):
+    """Consecutive batches of `batch` rows, each padded to round16(longest)
+    or to a fixed `seq`.  Returns a list of (ids, types, mask, seq)."""
+    out = []
+    for s in range(0, len(rows), batch):
+        chunk = rows[s:s + batch]
+        sq = round16(max(len(r) for r in chunk)) if seq is None else seq
+        ids, types, mask = pack(chunk, sq)
+        out.append((ids, types, mask, sq))
+    return out
+
+
 def varlen_mix(n: int = 2000, seed: int = 0, batch: int = 64):
     """consecutive batches of `batch` in seeded order, each padded
     to round16(longest).  Returns a list of (ids, types, mask, seq)."""
-    lengths = varlen_lengths(n, seed)
-    rng = np.random.default_rng(seed + 1)
-    rows = [sentence(rng, int(L)) for L in lengths]
-    out = []
-    for s in range(0, n, batch):
-        chunk = rows[s:s + batch]
-        seq = round16(max(len(r) for r in chunk))
-        ids, types, mask = pack(chunk, seq)
-        out.append((ids, types, mask, seq))
-    return out
+    return batches_of(varlen_rows(n, seed), batch)
+
+
+def varlen_sorted(n: int = 2000, seed: int = 0, batch: int = 64):
+    """The reference corpus benchmark's dynamic mode on the configs[3]
+    sentences (bench/corpus.cu:79-118): sentences stable-sorted by length,
+    batches of `batch`, each padded to max(16, round16(longest)).  Returns
+    (batches, order) with order[k] = the input index of sorted sentence k."""
+    rows = varlen_rows(n, seed)
+    order = np.argsort(np.asarray([len(r) for r in rows]), kind="stable")
+    return batches_of([rows[i] for i in order], batch), order
+
+
+def varlen_padded(n: int = 2000, seed: int = 0, batch: int = 64, seq: int = 128):
+    """The reference corpus benchmark's padded mode on the configs[3]
+    sentences (bench/corpus.cu:64-77): consecutive batches at seq 128."""
+    return batches_of(varlen_rows(n, seed), batch, seq)
 
 
 def long_batch(batch: int = 256, seq: int = 512, seed: int = 5, lo: int = 256):

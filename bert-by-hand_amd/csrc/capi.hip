@@ -289,6 +289,30 @@ struct Packed {
   int n, max_len;
 };
 
+// out = LN(A . W^T + bias + residual) over 384-wide rows: one kernel where
+// the GEMM tile owns whole rows, else the residual GEMM and a LayerNorm pass
+// over out, timed as two ops.
+bbh_status linear_residual_ln(OpTimer* t, hipStream_t s, int op, const f16* A, const f16* W,
+                              const f16* bias, const f16* residual, const f16* gamma,
+                              const f16* beta, f16* out, int M, int K, const char* what) {
+  const int H = BBH_HIDDEN;
+  bool fused;
+  const int tile = bbh::gemm_residual_ln_tile(M, K, &fused);
+  if (fused)
+    return timed_op(t, s, {op, tile, 1, M, H, K, 0.f}, [&] {
+      return check_launch(bbh::gemm_residual_ln(A, W, bias, residual, gamma, beta, out, M, K,
+                                                BBH_LAYER_NORM_EPS, s),
+                          what);
+    });
+  BBH_TRY(timed_op(t, s, {op, tile, 0, M, H, K, 0.f}, [&] {
+    return check_launch(bbh::gemm_residual(A, W, bias, residual, out, M, K, s), what);
+  }));
+  return timed_op(t, s, {BBH_OP_LAYERNORM, -1, 0, M, H, 0, 0.f}, [&] {
+    return check_launch(bbh::layernorm(out, nullptr, gamma, beta, out, M, H, BBH_LAYER_NORM_EPS, s),
+                        "residual layernorm");
+  });
+}
+
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
                                const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
                                OpTimer* t = nullptr, const Packed* pk = nullptr) {
@@ -313,13 +337,8 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
                           "attention");
     }));
   }
-  bool fused;
-  const int tile = bbh::gemm_residual_ln_tile(M, H, &fused);
-  return timed_op(t, s, {BBH_OP_O_PROJ_LN, tile, fused ? 1 : 0, M, H, H, 0.f}, [&] {
-    return check_launch(bbh::gemm_residual_ln(ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g, L.ln1_b,
-                                              out, M, H, BBH_LAYER_NORM_EPS, s),
-                        "o-proj gemm+ln");
-  });
+  return linear_residual_ln(t, s, BBH_OP_O_PROJ_LN, ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g,
+                            L.ln1_b, out, M, H, "o-proj gemm+ln");
 }
 
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
@@ -336,13 +355,8 @@ bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16*
     return check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, F, H, bbh::Act::kGelu, s),
                         "ffn1 gemm");
   }));
-  bool fused;
-  const int tile = bbh::gemm_residual_ln_tile(M, F, &fused);
-  return timed_op(t, s, {BBH_OP_FFN2_LN, tile, fused ? 1 : 0, M, H, F, 0.f}, [&] {
-    return check_launch(bbh::gemm_residual_ln(ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
-                                              L.ln2_b, out, M, F, BBH_LAYER_NORM_EPS, s),
-                        "ffn2 gemm+ln");
-  });
+  return linear_residual_ln(t, s, BBH_OP_FFN2_LN, ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
+                            L.ln2_b, out, M, F, "ffn2 gemm+ln");
 }
 
 bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
@@ -360,10 +374,13 @@ bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t*
   int M = 0;
   for (int g = 0; g < n_segs; ++g) {
     const Segment& sg = segs[g];
-    BBH_TRY(check_launch(bbh::embedding_ln(ids + tok[g], types + tok[g], m->word, m->pos, m->type,
-                                           m->emb_g, m->emb_b, ws->ping + sg.row * BBH_HIDDEN,
-                                           sg.batch, sg.seq, BBH_LAYER_NORM_EPS, s),
-                         "embedding+ln"));
+    BBH_TRY(timed_op(t, s, {BBH_OP_EMBED, -1, 0, sg.batch * sg.seq, sg.seq, 0, 0.f}, [&] {
+      return check_launch(bbh::embedding_ln(ids + tok[g], types + tok[g], m->word, m->pos,
+                                            m->type, m->emb_g, m->emb_b,
+                                            ws->ping + sg.row * BBH_HIDDEN, sg.batch, sg.seq,
+                                            BBH_LAYER_NORM_EPS, s),
+                          "embedding+ln");
+    }));
     M += sg.batch * sg.seq;
   }
   f16* cur = ws->ping;
@@ -380,10 +397,12 @@ bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t*
 bbh_status run_encode_packed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
                              const int32_t* types, const Packed& pk, int M, f16* final_out,
                              hipStream_t s, OpTimer* t = nullptr) {
-  BBH_TRY(check_launch(bbh::embedding_ln_packed(ids, types, m->word, m->pos, m->type, m->emb_g,
-                                                m->emb_b, ws->ping, ws->sents, pk.n,
-                                                BBH_LAYER_NORM_EPS, s),
-                       "embedding+ln (packed)"));
+  BBH_TRY(timed_op(t, s, {BBH_OP_EMBED, -1, 0, M, pk.max_len, 0, 0.f}, [&] {
+    return check_launch(bbh::embedding_ln_packed(ids, types, m->word, m->pos, m->type, m->emb_g,
+                                                 m->emb_b, ws->ping, ws->sents, pk.n,
+                                                 BBH_LAYER_NORM_EPS, s),
+                        "embedding+ln (packed)");
+  }));
   if (M == 0) return BBH_OK;
   f16* cur = ws->ping;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
@@ -1054,11 +1073,65 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     for (size_t k = 0; k < segs.size(); ++k) {
       const int i = runs[groups[g].runs[k]].first;
       f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
-      BBH_TRY(check_launch(bbh::pool_normalize(w->attn_out + segs[k].row * BBH_HIDDEN,
-                                               segs[k].mask, out, segs[k].batch, segs[k].seq,
-                                               pool->streams[j]),
-                           "pool+normalize"));
+      BBH_TRY(timed_op(pool->timer, pool->streams[j],
+                       {BBH_OP_POOL, -1, 0, segs[k].batch, segs[k].seq, 0, 0.f}, [&] {
+                         return check_launch(
+                             bbh::pool_normalize(w->attn_out + segs[k].row * BBH_HIDDEN,
+                                                 segs[k].mask, out, segs[k].batch, segs[k].seq,
+                                                 pool->streams[j]),
+                             "pool+normalize");
+                       }));
     }
+  }
+  for (int j = 0; j < used; ++j) {
+    BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
+    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
+  }
+  return BBH_OK;
+}
+
+bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids,
+                          const int32_t* types, const int32_t* mask, const int64_t* tok_offsets,
+                          const int* batch_sizes, const int* seqs, const int64_t* emb_rows,
+                          void* emb, int n_batches, bbh_stream_t stream) {
+  if (!pool || !m || !ids || !types || !mask || !tok_offsets || !batch_sizes || !seqs ||
+      !emb_rows || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed_each: null argument");
+  if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
+  if (!aligned(emb, 4)) return misaligned("bbh_embed_each emb");
+  const int n = (int)pool->streams.size();
+  for (int i = 0; i < n_batches; ++i) {
+    bbh_status st = check_shape(pool->ws[0], batch_sizes[i], seqs[i]);
+    if (st != BBH_OK) return fail(st, "batch " + std::to_string(i) + ": " + g_err);
+    if (tok_offsets[i] < 0 || emb_rows[i] < 0)
+      return fail(BBH_ERR_INVALID_ARG, "batch " + std::to_string(i) + ": negative offset");
+  }
+  if (n_batches == 0) return BBH_OK;
+  // Batch i goes, in batch order, to the stream with the fewest rows so far.
+  std::vector<size_t> load(n, 0);
+  std::vector<int> stream_of(n_batches);
+  for (int i = 0; i < n_batches; ++i) {
+    const int j = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+    stream_of[i] = j;
+    load[j] += (size_t)batch_sizes[i] * seqs[i];
+  }
+  const hipStream_t caller = S(stream);
+  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
+  const int used = n_batches < n ? n_batches : n;  // every batch so far went to an empty stream
+  for (int j = 0; j < used; ++j)
+    BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
+  for (int i = 0; i < n_batches; ++i) {
+    const int j = stream_of[i];
+    const hipStream_t st = pool->streams[j];
+    bbh_workspace* w = pool->ws[j];
+    const int32_t* mk = mask + tok_offsets[i];
+    BBH_TRY(run_encode(w, m, ids + tok_offsets[i], types + tok_offsets[i], mk, w->attn_out,
+                       batch_sizes[i], seqs[i], st, pool->timer));
+    f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
+    BBH_TRY(timed_op(pool->timer, st, {BBH_OP_POOL, -1, 0, batch_sizes[i], seqs[i], 0, 0.f}, [&] {
+      return check_launch(bbh::pool_normalize(w->attn_out, mk, out, batch_sizes[i], seqs[i], st),
+                          "pool+normalize");
+    }));
   }
   for (int j = 0; j < used; ++j) {
     BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
@@ -1094,6 +1167,12 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
       if (len < 0 || len > seqs[i])
         return fail(BBH_ERR_INVALID_ARG, at + "sentence " + std::to_string(j) + " length " +
                                              std::to_string(len) + " outside [0, seq]");
+      // Every forward must fit a workspace; the split below starts a forward
+      // at a sentence without looking at its length.
+      if ((size_t)len > cap)
+        return fail(BBH_ERR_CAPACITY, at + "sentence " + std::to_string(j) + " length " +
+                                          std::to_string(len) + " exceeds the pool workspace's " +
+                                          std::to_string(cap) + " rows");
       all.push_back({tok_offsets[i] + (int64_t)j * seqs[i], emb_rows[i] + j, 0, len});
       total += (size_t)len;
     }
@@ -1163,9 +1242,11 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
     sl.pending[j] = true;
     const Packed pk{(int)cnt, max_len};
     BBH_TRY(run_encode_packed(w, m, ids, types, pk, M, w->attn_out, st, pool->timer));
-    BBH_TRY(check_launch(bbh::pool_normalize_packed(w->attn_out, w->sents, (int)cnt,
-                                                    static_cast<f16*>(emb), st),
-                         "pool+normalize (packed)"));
+    BBH_TRY(timed_op(pool->timer, st, {BBH_OP_POOL, -1, 0, (int)cnt, max_len, 0, 0.f}, [&] {
+      return check_launch(bbh::pool_normalize_packed(w->attn_out, w->sents, (int)cnt,
+                                                     static_cast<f16*>(emb), st),
+                          "pool+normalize (packed)");
+    }));
   }
   for (int j = 0; j < used; ++j) {
     BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
@@ -1234,7 +1315,7 @@ static bbh_status layer_from(const bbh_attn_weights* a, const bbh_ffn_weights* f
     if (!a->qkv_w || !a->qkv_b || !a->o_w || !a->o_b || !a->ln_w || !a->ln_b)
       return fail(BBH_ERR_INVALID_ARG, "null attention weight pointer");
     if (!aligned(a->qkv_w, 16) || !aligned(a->o_w, 16) || !aligned(a->qkv_b, 8) ||
-        !aligned(a->o_b, 8) || !aligned(a->ln_w, 8) || !aligned(a->ln_b, 8))
+        !aligned(a->o_b, 16) || !aligned(a->ln_w, 16) || !aligned(a->ln_b, 16))
       return misaligned("attention weights");
     L->qkv_w = static_cast<const f16*>(a->qkv_w);
     L->qkv_b = static_cast<const f16*>(a->qkv_b);
@@ -1247,7 +1328,7 @@ static bbh_status layer_from(const bbh_attn_weights* a, const bbh_ffn_weights* f
     if (!f->inter_w || !f->inter_b || !f->out_w || !f->out_b || !f->ln_w || !f->ln_b)
       return fail(BBH_ERR_INVALID_ARG, "null ffn weight pointer");
     if (!aligned(f->inter_w, 16) || !aligned(f->out_w, 16) || !aligned(f->inter_b, 8) ||
-        !aligned(f->out_b, 8) || !aligned(f->ln_w, 8) || !aligned(f->ln_b, 8))
+        !aligned(f->out_b, 16) || !aligned(f->ln_w, 16) || !aligned(f->ln_b, 16))
       return misaligned("ffn weights");
     L->f1_w = static_cast<const f16*>(f->inter_w);
     L->f1_b = static_cast<const f16*>(f->inter_b);
@@ -1360,8 +1441,8 @@ bbh_status bbh_linear_residual_layernorm(const void* A, const void* B, const voi
   if (M < 1 || K < 1) return fail(BBH_ERR_INVALID_ARG, "M and K must be positive");
   if (N != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "N must be 384");
   if (K % 64 != 0) return fail(BBH_ERR_UNSUPPORTED, "K must be a multiple of 64");
-  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(bias, 8) || !aligned(residual, 8) ||
-      !aligned(gamma, 8) || !aligned(beta, 8) || !aligned(y, 8))
+  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(bias, 16) || !aligned(residual, 16) ||
+      !aligned(gamma, 16) || !aligned(beta, 16) || !aligned(y, 16))
     return misaligned("bbh_linear_residual_layernorm");
   return check_launch(
       bbh::gemm_residual_ln(static_cast<const f16*>(A), static_cast<const f16*>(B),

@@ -928,47 +928,37 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 }
 
 // Tile configurations (BM, BN, wavefronts M x N, A-ring depth), by id; the K
-// slice is 64 wide and the W ring 2 deep throughout.
+// slice is 64 wide and the W ring 2 deep throughout.  The product build holds
+// the configurations pick_plain and gemm_residual_ln_tile choose; the others
+// of the sweep that chose them are compiled only with -DBBH_TUNING.
 //   id  tile      wave tile  SA   LDS
 //    0  64x64     32x32      4    48 KB
-//    1  64x128    32x64      4    64 KB
-//    2  128x64    64x32      4    80 KB
-//    3  128x128   64x64      4    96 KB
-//    4  256x128   128x64     3   128 KB
-//    5  128x384   128x96     4   160 KB   (owns whole 384-wide rows)
-//    6  64x384    64x96      4   128 KB   (owns whole rows)
-//    7  32x128    32x32      4    48 KB
-//    8  128x192   64x96      4   112 KB
-//    9  256x192   128x96     3   144 KB
-//   10  32x384    32x96      4   112 KB   (owns whole rows)
-//   11  128x384   128x96     3   144 KB   (owns whole rows)
-//   12  256x192   128x96     2   112 KB
-//   13  128x192   64x96      3    96 KB
-//   14  64x384    64x96      2   112 KB   (owns whole rows)
-//   15  128x128   64x64      2    64 KB
-//   16  64x128    32x64      6    80 KB
+//   14  64x384    64x96      2   112 KB   (owns whole 384-wide rows)
 //   8 wavefronts (2 per SIMD):
-//   17  256x384   128x96     2   160 KB   (owns whole rows)
 //   18  128x384   64x96      4   160 KB   (owns whole rows)
 //   19  256x192   64x96      3   144 KB
-//   20  256x128   64x64      3   128 KB
-//   21  128x256   64x64      4   128 KB
 //   register-staged K slices (PD slices in flight in VGPRs, LDS double buffer):
-//   22  128x128   64x64      PD 3   64 KB
-//   23  128x128   64x64      PD 4   64 KB
-//   24  128x256   64x64 (8w) PD 2   96 KB
-//   25  256x128   64x64 (8w) PD 2   96 KB
 //   26  64x64     32x32      PD 4   32 KB
-//   27  128x192   64x96      PD 3   80 KB
 //   28  128x384   64x96 (8w) PD 2  128 KB   (owns whole rows)
-//   29  256x128   128x64     PD 3   96 KB
 //   30  128x128   64x32 (8w) PD 2   64 KB
 //   31  128x128   32x64 (8w) PD 2   64 KB
 //   32  128x192   32x96 (8w) PD 2   80 KB
 // Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD,SW>, epilogue>.
-// The table itself: X(id, BM, BN, WM, WN, SA, PD, SW), ids dense from 0.
+// The table itself: X(id, BM, BN, WM, WN, SA, PD, SW).
 #define BBH_TILES(X) \
   X(0, 64, 64, 2, 2, 4, 0, 2) \
+  X(14, 64, 384, 1, 4, 2, 0, 2) \
+  X(18, 128, 384, 2, 4, 4, 0, 2) \
+  X(19, 256, 192, 4, 2, 3, 0, 2) \
+  X(26, 64, 64, 2, 2, 2, 4, 2) \
+  X(28, 128, 384, 2, 4, 2, 2, 2) \
+  X(30, 128, 128, 2, 4, 2, 2, 2) \
+  X(31, 128, 128, 4, 2, 2, 2, 2) \
+  X(32, 128, 192, 4, 2, 2, 2, 2)
+
+#ifdef BBH_TUNING
+// The rest of the sweep (ids 1-13, 15-17, 20-25, 27, 29).
+#define BBH_TUNING_TILES(X) \
   X(1, 64, 128, 2, 2, 4, 0, 2) \
   X(2, 128, 64, 2, 2, 4, 0, 2) \
   X(3, 128, 128, 2, 2, 4, 0, 2) \
@@ -982,25 +972,22 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
   X(11, 128, 384, 1, 4, 3, 0, 2) \
   X(12, 256, 192, 2, 2, 2, 0, 2) \
   X(13, 128, 192, 2, 2, 3, 0, 2) \
-  X(14, 64, 384, 1, 4, 2, 0, 2) \
   X(15, 128, 128, 2, 2, 2, 0, 2) \
   X(16, 64, 128, 2, 2, 6, 0, 2) \
   X(17, 256, 384, 2, 4, 2, 0, 2) \
-  X(18, 128, 384, 2, 4, 4, 0, 2) \
-  X(19, 256, 192, 4, 2, 3, 0, 2) \
   X(20, 256, 128, 4, 2, 3, 0, 2) \
   X(21, 128, 256, 2, 4, 4, 0, 2) \
   X(22, 128, 128, 2, 2, 2, 3, 2) \
   X(23, 128, 128, 2, 2, 2, 4, 2) \
   X(24, 128, 256, 2, 4, 2, 2, 2) \
   X(25, 256, 128, 4, 2, 2, 2, 2) \
-  X(26, 64, 64, 2, 2, 2, 4, 2) \
   X(27, 128, 192, 2, 2, 2, 3, 2) \
-  X(28, 128, 384, 2, 4, 2, 2, 2) \
-  X(29, 256, 128, 2, 2, 2, 3, 2) \
-  X(30, 128, 128, 2, 4, 2, 2, 2) \
-  X(31, 128, 128, 4, 2, 2, 2, 2) \
-  X(32, 128, 192, 4, 2, 2, 2, 2)
+  X(29, 256, 128, 2, 2, 2, 3, 2)
+#else
+#define BBH_TUNING_TILES(X)
+#endif
+
+constexpr int kTiles = 33;  // ids 0 .. 32; kTiles names the weight-resident kernel
 
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
@@ -1010,20 +997,37 @@ hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const 
   case ID:                                                                           \
     return launch<Cfg<BM, BN, WM, WN, SA, PD, SW>, EPI>(A, W, bias, residual, gamma, \
                                                         beta, out, M, N, K, eps, s);
-  switch (id) { BBH_TILES(BBH_CASE) }
+  switch (id) {
+    BBH_TILES(BBH_CASE)
+    BBH_TUNING_TILES(BBH_CASE)
+  }
 #undef BBH_CASE
   return hipErrorInvalidValue;
 }
 
-#define BBH_BN(ID, BM, BN, WM, WN, SA, PD, SW) BN,
-constexpr int kBnOf[] = {BBH_TILES(BBH_BN)};
+int bn_of(int id) {
+#define BBH_BN(ID, BM, BN, WM, WN, SA, PD, SW) \
+  case ID:                                     \
+    return BN;
+  switch (id) {
+    BBH_TILES(BBH_BN)
+    BBH_TUNING_TILES(BBH_BN)
+  }
 #undef BBH_BN
-constexpr int kTiles = sizeof(kBnOf) / sizeof(kBnOf[0]);
+  return 0;
+}
 
+const char* tile_name(int id) {
 #define BBH_NAME(ID, BM, BN, WM, WN, SA, PD, SW) \
-  "Cfg<" #BM "," #BN "," #WM "," #WN "," #SA "," #PD "," #SW ">",
-const char* const kTileName[] = {BBH_TILES(BBH_NAME)};
+  case ID:                                       \
+    return "Cfg<" #BM "," #BN "," #WM "," #WN "," #SA "," #PD "," #SW ">";
+  switch (id) {
+    BBH_TILES(BBH_NAME)
+    BBH_TUNING_TILES(BBH_NAME)
+  }
 #undef BBH_NAME
+  return nullptr;
+}
 
 // Tile config per shape, from interleaved A/B timings (medians of several
 // rounds) on MI355X over the encoder's four shapes (N, K) = (1152, 384) QKV,
@@ -1049,8 +1053,8 @@ int pick_plain(int M, int N, int K) {
   else if (M <= 49152)
     id = wide_k ? 19 : 30;
   else
-    id = qkv ? 17 : ffn1 ? 31 : wide_k ? 17 : 30;
-  return (N % kBnOf[id] == 0) ? id : 0;  // id 0 takes any N % 64 == 0
+    id = qkv ? 19 : ffn1 ? 31 : wide_k ? 19 : 30;
+  return (N % bn_of(id) == 0) ? id : 0;  // id 0 takes any N % 64 == 0
 }
 
 }  // namespace
@@ -1078,7 +1082,8 @@ int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
 
 const char* gemm_tile_name(int tile) {
   if (tile == kTiles) return "WRes<12x32,384>";
-  return (tile >= 0 && tile < kTiles) ? kTileName[tile] : "generic";
+  const char* n = tile_name(tile);
+  return n ? n : "generic";
 }
 
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N, int K,
@@ -1108,10 +1113,17 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f
     return launch_wres<kLayerNorm>(A, W, bias, y, M, kHidden, s, residual, gamma, beta, eps);
   if (fused)
     return launch_id<kLayerNorm>(id, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
-  hipError_t e = launch_id<kResidual>(id, A, W, bias, residual, nullptr, nullptr, y, M, kHidden, K,
-                                      eps, s);
+  hipError_t e = gemm_residual(A, W, bias, residual, y, M, K, s);
   if (e != hipSuccess) return e;
   return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);
+}
+
+hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,
+                         int M, int K, hipStream_t s) {
+  bool fused;
+  const int id = gemm_residual_ln_tile(M, K, &fused);
+  if (fused) return hipErrorInvalidValue;
+  return launch_id<kResidual>(id, A, W, bias, residual, nullptr, nullptr, y, M, kHidden, K, 0.f, s);
 }
 
 #ifdef BBH_TUNING

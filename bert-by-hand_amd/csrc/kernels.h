@@ -38,6 +38,12 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
                             const f16* residual, const f16* gamma, const f16* beta,
                             f16* y, int M, int K, float eps, hipStream_t s);
 
+// The first half of gemm_residual_ln where gemm_residual_ln_tile says the
+// LayerNorm is not fused: y = A . W^T + bias + residual (fp16), which a
+// layernorm(y, ...) pass then normalises in place.
+hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,
+                         int M, int K, hipStream_t s);
+
 // Fused masked attention from the QKV activations (row stride 3*heads*32).
 hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
                      int heads, int seq, float scale, hipStream_t s);

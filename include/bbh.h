@@ -185,6 +185,21 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
                              const int *seqs, const int64_t *emb_rows, void *emb,
                              int n_batches, bbh_stream_t stream);
 
+/* bbh_embed_each: the reference's corpus loop (bench/corpus.cu:64-77,
+ * 120-132), one bert_embed per batch, with the batches spread over the pool
+ * streams.  Same arguments as bbh_embed_batches, but every batch is its own
+ * forward at its own (batch_sizes[i], seqs[i]) shape: nothing is merged and
+ * every padding row is computed, so each batch's embeddings are bit for bit
+ * those of bbh_embed on that batch.  Batch i goes, in batch order, to the
+ * stream with the fewest rows so far; the call orders itself after prior
+ * work on `stream`, makes later work on `stream` wait for all batches, and
+ * returns without a host sync. */
+bbh_status bbh_embed_each(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
+                          const int32_t *types, const int32_t *mask,
+                          const int64_t *tok_offsets, const int *batch_sizes, const int *seqs,
+                          const int64_t *emb_rows, void *emb, int n_batches,
+                          bbh_stream_t stream);
+
 /* bbh_embed_packed: the embeddings bbh_embed_batches gives for the same
  * batches when every mask is right padding (the tokenizer's layout: ones,
  * then zeros), computed without the padding rows.  lengths (HOST array, one
@@ -202,6 +217,8 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
  * Sentences are split, in order, into one forward per pool stream of about
  * equal token counts (more if a forward would exceed a workspace's
  * max_batch*max_seq tokens or sentences); seqs need not be multiples of 16.
+ * A sentence longer than a workspace's max_batch*max_seq rows is rejected
+ * with BBH_ERR_CAPACITY before anything is enqueued.
  * Each call uploads its sentence table from pinned memory; the call orders
  * itself after prior work on `stream`, makes later work on `stream` wait,
  * and returns without a host sync, except that it waits for the plan copies
@@ -213,7 +230,8 @@ bbh_status bbh_embed_packed(bbh_pool *pool, const bbh_model *m, const int32_t *i
                             bbh_stream_t stream);
 
 /* ---- per-launch timing of a pool ---------------------------------------------
- * HIP-event timing of each encoder op that bbh_embed_batches launches (the
+ * HIP-event timing of each op that bbh_embed_batches, bbh_embed_each and
+ * bbh_embed_packed launch (the
  * reference times whole forwards with CUDA events, src/core/timer.h:36-39).
  * bbh_pool_timing(pool, capacity) starts a new record: a pair of events goes
  * on the launching pool stream around every op of every forward, for the
@@ -224,15 +242,20 @@ bbh_status bbh_embed_packed(bbh_pool *pool, const bbh_model *m, const int32_t *i
 typedef enum bbh_op {
   BBH_OP_QKV = 1,       /* fused QKV Linear */
   BBH_OP_ATTENTION = 2, /* masked multi-head attention */
-  BBH_OP_O_PROJ_LN = 3, /* attention output Linear + residual LayerNorm */
+  BBH_OP_O_PROJ_LN = 3, /* attention output Linear + residual (+ LayerNorm when fused) */
   BBH_OP_FFN1_GELU = 4, /* intermediate Linear + GELU */
-  BBH_OP_FFN2_LN = 5    /* output Linear + residual LayerNorm */
+  BBH_OP_FFN2_LN = 5,   /* output Linear + residual (+ LayerNorm when fused) */
+  BBH_OP_EMBED = 6,     /* embedding gather + embedding LayerNorm */
+  BBH_OP_POOL = 7,      /* masked mean pool + L2 normalize */
+  BBH_OP_LAYERNORM = 8  /* residual LayerNorm pass after an unfused O-proj / FFN2 */
 } bbh_op;
 typedef struct bbh_launch_time {
   int op;       /* bbh_op */
-  int tile;     /* GEMM tile configuration (bbh_gemm_tile_name); -1 for attention */
-  int fused_ln; /* LayerNorm ops: 1 inside the GEMM kernel, 0 a second kernel timed with it */
-  int m, n, k;  /* GEMM (M, N, K); attention (batch, seq, heads) */
+  int tile;     /* GEMM tile configuration (bbh_gemm_tile_name); -1 for other ops */
+  int fused_ln; /* O-proj / FFN2: 1 when the LayerNorm runs inside the GEMM kernel, 0 when it
+                   follows as its own BBH_OP_LAYERNORM record */
+  int m, n, k;  /* GEMM (M, N, K); attention (batch, seq, heads); embed / pool / LayerNorm
+                   (rows or sentences, seq or 384, 0) */
   float ms;     /* time between the pair of events */
 } bbh_launch_time;
 bbh_status bbh_pool_timing(bbh_pool *pool, int capacity);
@@ -243,8 +266,10 @@ const char *bbh_gemm_tile_name(int tile);
 
 /* ---- weight views (src/model/encoder.h:11-22,37-40) -------------------------
  * Device pointers of one encoder layer's fp16 tensors, the reference's
- * AttnWeights / FfnWeights field for field.  Matrices must be 16-byte
- * aligned and vectors 8-byte aligned (every hipMalloc'd buffer is). */
+ * AttnWeights / FfnWeights field for field.  Matrices, the output-dense
+ * biases and the LayerNorm vectors must be 16-byte aligned (the fused
+ * LayerNorm epilogues read them 16 bytes at a time), the QKV and intermediate
+ * biases 8-byte aligned; every hipMalloc'd buffer is. */
 typedef struct bbh_attn_weights {
   const void *qkv_w, *qkv_b; /* (1152, 384) with Q|K|V row blocks, (1152) */
   const void *o_w, *o_b;     /* attention output dense (384, 384), (384) */
@@ -294,7 +319,9 @@ bbh_status bbh_linear(const void *A, const void *B, void *C, int M, int N, int K
 /* Linear + bias + residual + LayerNorm in one kernel (the fused tail of
  * attention_block / ffn_block, src/model/encoder.cu:47-50,61-64):
  * y = LN(A . B^T + bias + residual) * gamma + beta, N must be 384 and K a
- * multiple of 64.  y may alias residual. */
+ * multiple of 64.  y may alias residual.  Every pointer must be 16-byte
+ * aligned (the epilogue moves residual, y, bias, gamma and beta in 16-byte
+ * pieces). */
 bbh_status bbh_linear_residual_layernorm(const void *A, const void *B,
                                          const void *bias, const void *residual,
                                          const void *gamma, const void *beta,

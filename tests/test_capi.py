@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 51
+    assert len(names) == 52
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point
@@ -156,8 +156,11 @@ def test_weight_view_entry_points_validate_before_launch():
 
 def test_tile_names_and_timing_arguments():
     L = _lib()
-    assert L.bbh_gemm_tile_name(23) == b"Cfg<128,128,2,2,2,4,2>"
+    assert L.bbh_gemm_tile_name(26) == b"Cfg<64,64,2,2,2,4,2>"
     assert L.bbh_gemm_tile_name(0) == b"Cfg<64,64,2,2,4,0,2>"
+    assert L.bbh_gemm_tile_name(33) == b"WRes<12x32,384>"
+    # sweep-only configurations are not in the product build
+    assert L.bbh_gemm_tile_name(23) == b"generic"
     assert L.bbh_gemm_tile_name(-1) == b"generic" and L.bbh_gemm_tile_name(999) == b"generic"
     cnt = ctypes.c_int(7)
     assert L.bbh_pool_timing(None, 16) == 1

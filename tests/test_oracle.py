@@ -207,3 +207,39 @@ def test_synthetic_inputs_match_recorded_statistics():
     # FLOPs(B, s) = B*s*21,233,664 + B*9,216*s^2: 21.89 G at B64 s16, 3,401.6 G at B256 s512
     assert synth.flops_per_forward(64, 16) == 21_894_266_880
     assert abs(synth.flops_per_forward(256, 512) / 1e9 - 3401.6) < 0.1
+
+
+@pytest.mark.parametrize("tag", ["s16", "rag"])
+def test_torch_cpu_forward_matches_golden_and_oracle(weights32, golden_model, tag):
+    # The CPU baseline's forward (transformers BertModel, sdpa attention) on
+    # the seeded weights gives the committed golden embeddings (written by the
+    # eager BertModel) and the numpy oracle's.
+    from oracle import torch_forward as T
+
+    g = golden_model
+    ids, types, mask = g[f"{tag}_ids"], g[f"{tag}_types"], g[f"{tag}_mask"]
+    got = T.embed(T.build(weights32), ids, types, mask)
+    assert np.abs(got - g[f"{tag}_embedding"]).max() < 1e-5
+    assert np.abs(got - O.bert_embed(weights32, ids, types, mask)).max() < 1e-5
+
+
+def test_corpus_modes_follow_reference_batching():
+    # bench/corpus.cu:64-77 (every batch at seq 128) and :79-118 (length-sorted,
+    # each batch at max(16, round16(longest))) on the configs[3] sentences.
+    from bbh import synth
+
+    rows = synth.varlen_rows()
+    lens = np.array([len(r) for r in rows])
+    sorted_b, order = synth.varlen_sorted()
+    assert sorted(order.tolist()) == list(range(2000))
+    assert np.all(np.diff(lens[order]) >= 0)
+    got = [row for b in sorted_b for row in b[0]]
+    assert all(np.array_equal(got[k][:lens[i]], rows[i]) and not got[k][lens[i]:].any()
+               for k, i in enumerate(order))
+    effs = [b[3] for b in sorted_b]
+    assert effs == [max(16, -(-int(lens[order[s:s + 64]].max()) // 16) * 16)
+                    for s in range(0, 2000, 64)]
+    assert sum(b[0].shape[0] * b[3] for b in sorted_b) == 41984
+    padded = synth.varlen_padded()
+    assert all(b[3] == 128 and b[0].shape[1] == 128 for b in padded)
+    assert np.array_equal(np.concatenate([b[2].sum(1) for b in padded]), lens)

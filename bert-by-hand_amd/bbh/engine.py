@@ -179,7 +179,7 @@ class Pool:
         call("bbh_pool_timing_read", self.handle, None, 0, ctypes.byref(cnt))
         buf = (capi.LaunchTime * max(cnt.value, 1))()
         call("bbh_pool_timing_read", self.handle, buf, cnt.value, ctypes.byref(cnt))
-        return [dict(op=self.OPS[r.op], tile=r.tile, fused_ln=bool(r.fused_ln), m=r.m, n=r.n,
+        return [dict(op=self.OPS[r.op], tile=r.tile, fused_ln=int(r.fused_ln), m=r.m, n=r.n,
                      k=r.k, ms=r.ms) for r in buf[:cnt.value]]
 
     def close(self):

@@ -1566,6 +1566,7 @@ bbh_status bbh_pool_normalize(const void* hidden, const int32_t* mask, void* out
   if (!hidden || !mask || !out) return fail(BBH_ERR_INVALID_ARG, "null argument");
   if (dim != BBH_HIDDEN) return fail(BBH_ERR_UNSUPPORTED, "dim must be 384");
   if (seq < 1 || batch < 1) return fail(BBH_ERR_INVALID_ARG, "bad sizes");
+  if (seq > BBH_MAX_POSITION) return fail(BBH_ERR_CAPACITY, "seq exceeds max position 512");
   if (!aligned(hidden, 4) || !aligned(out, 4)) return misaligned("bbh_pool_normalize");
   return check_launch(bbh::pool_normalize(static_cast<const f16*>(hidden), mask,
                                           static_cast<f16*>(out), batch, seq, S(stream)),

@@ -83,6 +83,55 @@ __device__ inline float gelu_poly(float x) {
   return x * fmaf(u, p, 0.5f);
 }
 
+// LayerNorm of one 384-wide row held by a wavefront: lane l holds columns
+// 2l + 128j (j = 0, 1, 2) as v[2j], v[2j+1].  Two-pass mean and variance over
+// the registers (src/kernels/layernorm.cu:32-49 reads the row three times);
+// on return v holds (v - mean) * rstd.
+__device__ __forceinline__ void ln_row384(float (&v)[6], float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 6; ++e) s += v[e];
+  const float mean = wave_sum(s) * (1.0f / kHidden);
+  float q = 0.f;
+#pragma unroll
+  for (int e = 0; e < 6; ++e) {
+    v[e] -= mean;
+    q += v[e] * v[e];
+  }
+  const float rstd = rsqrtf(wave_sum(q) * (1.0f / kHidden) + eps);
+#pragma unroll
+  for (int e = 0; e < 6; ++e) v[e] *= rstd;
+}
+
+// gamma / beta of a lane's columns (layout of ln_row384), loaded before the
+// row so that their latency overlaps the row's instead of following the
+// reductions.
+struct Affine384 {
+  f16x2 g[3], b[3];
+};
+__device__ __forceinline__ Affine384 load_affine384(const f16* __restrict__ gamma,
+                                                    const f16* __restrict__ beta, int lane) {
+  Affine384 a;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    a.g[j] = *reinterpret_cast<const f16x2*>(gamma + 2 * lane + 128 * j);
+    a.b[j] = *reinterpret_cast<const f16x2*>(beta + 2 * lane + 128 * j);
+  }
+  return a;
+}
+
+// y[c] = v * gamma[c] + beta[c] for the lane's columns.
+__device__ __forceinline__ void store_affine384(f16* __restrict__ y, const float (&v)[6],
+                                                const Affine384& a, int lane) {
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    f16x2 o;
+    o[0] = (f16)(v[2 * j] * (float)a.g[j][0] + (float)a.b[j][0]);
+    o[1] = (f16)(v[2 * j + 1] * (float)a.g[j][1] + (float)a.b[j][1]);
+    *reinterpret_cast<f16x2*>(y + 2 * lane + 128 * j) = o;
+  }
+}
+
 // D(16x16, fp32) += A(16x32, fp16) . B(32x16, fp16) on the CDNA4 matrix core.
 // Lane l supplies row (l % 16) of A and column (l % 16) of B, each as 8
 // consecutive k values of k-group (l / 16); it receives D rows

@@ -8,43 +8,14 @@
 // registers (two-pass, as src/kernels/layernorm.cu:32-49, but one global read
 // instead of three).
 
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace bbh {
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one row per wavefront, 256 threads
-
-__device__ __forceinline__ void ln_row384(float (&v)[6], float eps) {
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 6; ++e) s += v[e];
-  const float mean = wave_sum(s) * (1.0f / kHidden);
-  float q = 0.f;
-#pragma unroll
-  for (int e = 0; e < 6; ++e) {
-    v[e] -= mean;
-    q += v[e] * v[e];
-  }
-  const float rstd = rsqrtf(wave_sum(q) * (1.0f / kHidden) + eps);
-#pragma unroll
-  for (int e = 0; e < 6; ++e) v[e] *= rstd;
-}
-
-__device__ __forceinline__ void store_affine384(f16* __restrict__ y, const float (&v)[6],
-                                                const f16* __restrict__ gamma,
-                                                const f16* __restrict__ beta, int lane) {
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int c = 2 * lane + 128 * j;
-    const f16x2 gv = *reinterpret_cast<const f16x2*>(gamma + c);
-    const f16x2 bv = *reinterpret_cast<const f16x2*>(beta + c);
-    f16x2 o;
-    o[0] = (f16)(v[2 * j] * (float)gv[0] + (float)bv[0]);
-    o[1] = (f16)(v[2 * j + 1] * (float)gv[1] + (float)bv[1]);
-    *reinterpret_cast<f16x2*>(y + c) = o;
-  }
-}
 
 // y = LN(x [+ residual]) for D == 384 (src/kernels/layernorm.cu:17-59).
 __global__ __launch_bounds__(256) void ln384_kernel(const f16* x, const f16* residual,
@@ -54,6 +25,7 @@ __global__ __launch_bounds__(256) void ln384_kernel(const f16* x, const f16* res
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   const size_t off = (size_t)row * kHidden;
+  const Affine384 aff = load_affine384(gamma, beta, lane);
   float v[6];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
@@ -68,7 +40,7 @@ __global__ __launch_bounds__(256) void ln384_kernel(const f16* x, const f16* res
     }
   }
   ln_row384(v, eps);
-  store_affine384(y + off, v, gamma, beta, lane);
+  store_affine384(y + off, v, aff, lane);
 }
 
 // Any D: three strided passes per wavefront-owned row, fp32 statistics.
@@ -107,6 +79,7 @@ __device__ __forceinline__ void embed_row(int id_raw, int tt_raw, int p, const f
   const f16* wr = word + (size_t)id * kHidden;
   const f16* pr = pos + (size_t)p * kHidden;
   const f16* tr = type + (size_t)tt * kHidden;
+  const Affine384 aff = load_affine384(gamma, beta, lane);
   float v[6];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
@@ -118,7 +91,7 @@ __device__ __forceinline__ void embed_row(int id_raw, int tt_raw, int p, const f
     v[2 * j + 1] = (float)a[1] + (float)q[1] + (float)t[1];
   }
   ln_row384(v, eps);
-  store_affine384(dst, v, gamma, beta, lane);
+  store_affine384(dst, v, aff, lane);
 }
 
 // out[row] = LN(word[id] + pos[row % seq] + type[tt]) (src/model/forward.cu:28-31;
@@ -165,34 +138,58 @@ __global__ __launch_bounds__(256) void embedding_kernel(
 }
 
 // One workgroup per sentence: the four wavefronts sum disjoint sets of tokens
-// (positions w, w+4, ...) of the masked mean, combine through LDS, then wave 0
-// divides by max(count, 1) (src/kernels/pooling.cu:21-31) and scales by
-// 1 / max(||x||, 1e-12) (src/kernels/normalize.cu:7,29-30).  `row(p)` is the
-// hidden row of position p, or null for a masked position.
-template <class RowOf>
-__device__ __forceinline__ void pool_normalize_body(int seq, RowOf row, f16* __restrict__ dst) {
+// (positions w, w+4, ... in increasing order) of the masked mean, combine
+// through LDS, then wave 0 divides by max(count, 1) (src/kernels/pooling.cu:
+// 21-31) and scales by 1 / max(||x||, 1e-12) (src/kernels/normalize.cu:7,
+// 29-30).  `valid(p)` says whether position p is counted and `row(p)` is its
+// hidden row.  Each wavefront first lists its counted positions in LDS (one
+// ballot per 64 of them), then sums their rows four at a time, so the row
+// loads are issued together instead of one mask-dependent load at a time; the
+// sum order is the same as one position after another.
+template <class Valid, class RowOf>
+__device__ __forceinline__ void pool_normalize_body(int seq, Valid valid, RowOf row,
+                                                    f16* __restrict__ dst) {
   __shared__ float part[4][kHidden];
   __shared__ int cnt_part[4];
+  __shared__ short plist[4][kMaxPos / 4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int cnt = 0;
-  for (int s = wave; s < seq; s += 4) {
-    const f16* hr = row(s);
-    if (!hr) continue;
-    ++cnt;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const f16x2 a = *reinterpret_cast<const f16x2*>(hr + 2 * lane + 128 * j);
-      acc[2 * j] += (float)a[0];
-      acc[2 * j + 1] += (float)a[1];
-    }
+  int n = 0;
+  for (int i0 = 0; i0 < (seq + 3) / 4; i0 += kWave) {
+    const int p = wave + 4 * (i0 + lane);
+    const bool v = p < seq && valid(p);
+    const uint64_t bal = __ballot(v);
+    if (v) plist[wave][n + __popcll(bal & ((1ull << lane) - 1))] = (short)p;
+    n += __popcll(bal);
   }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's list is in LDS
+  __builtin_amdgcn_wave_barrier();
+  float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto add_rows = [&](auto cnt_c, int k) {
+    constexpr int U = decltype(cnt_c)::value;
+    f16x2 a[U][3];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const f16* hr = row(plist[wave][k + u]);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) a[u][j] = *reinterpret_cast<const f16x2*>(hr + 2 * lane + 128 * j);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        acc[2 * j] += (float)a[u][j][0];
+        acc[2 * j + 1] += (float)a[u][j][1];
+      }
+  };
+  int k = 0;
+  for (; k + 4 <= n; k += 4) add_rows(std::integral_constant<int, 4>{}, k);
+  for (; k < n; ++k) add_rows(std::integral_constant<int, 1>{}, k);
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
     part[wave][2 * lane + 128 * j] = acc[2 * j];
     part[wave][2 * lane + 128 * j + 1] = acc[2 * j + 1];
   }
-  if (lane == 0) cnt_part[wave] = cnt;
+  if (lane == 0) cnt_part[wave] = n;
   __syncthreads();
   if (wave != 0) return;
   const int total = cnt_part[0] + cnt_part[1] + cnt_part[2] + cnt_part[3];
@@ -223,7 +220,7 @@ __global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restri
   const f16* hb = hidden + (size_t)b * seq * kHidden;
   const int32_t* mb = mask + (size_t)b * seq;
   pool_normalize_body(
-      seq, [&](int p) { return mb[p] != 0 ? hb + (size_t)p * kHidden : nullptr; },
+      seq, [&](int p) { return mb[p] != 0; }, [&](int p) { return hb + (size_t)p * kHidden; },
       out + (size_t)b * kHidden);
 }
 
@@ -234,7 +231,8 @@ __global__ __launch_bounds__(256) void pool_normalize_packed_kernel(
   const PackedSentence sn = sents[blockIdx.x];
   const f16* hb = hidden + (size_t)sn.row * kHidden;
   pool_normalize_body(
-      sn.len, [&](int p) { return hb + (size_t)p * kHidden; }, out + (size_t)sn.out_row * kHidden);
+      sn.len, [&](int) { return true; }, [&](int p) { return hb + (size_t)p * kHidden; },
+      out + (size_t)sn.out_row * kHidden);
 }
 
 // out[b, d] = masked mean over seq, any dim (src/kernels/pooling.cu:8-32).

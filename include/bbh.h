@@ -376,7 +376,7 @@ bbh_status bbh_mean_pool(const void *hidden, const int32_t *mask, void *out,
                          int seq, int dim, int batch, bbh_stream_t stream);
 /* launch_l2_normalize (normalize.h:7): rows of x /= max(||x||, 1e-12). */
 bbh_status bbh_l2_normalize(void *x, int n, int batch, bbh_stream_t stream);
-/* Masked mean pool + L2 normalize fused (forward.cu:51-52), dim 384. */
+/* Masked mean pool + L2 normalize fused (forward.cu:51-52), dim 384, seq <= 512. */
 bbh_status bbh_pool_normalize(const void *hidden, const int32_t *mask, void *out,
                               int seq, int dim, int batch, bbh_stream_t stream);
 /* launch_gelu (src/kernels/gelu.h:9): x[i] = GELU(x[i]) in place, exact erf

@@ -407,3 +407,52 @@ def test_pool_normalize(torch_cuda, B, S):
     assert np.abs(_np(pooled) - want).max() <= 2e-3
     if B > 2:
         assert np.all(got[2] == 0.0)
+
+
+@pytest.mark.parametrize("B,S", [(1, 16), (64, 16), (31, 48), (64, 48), (64, 64), (96, 64), (64, 128)])
+def test_workspace_residual_layernorm_equals_two_pass(torch_cuda, ws, model, weights32, B, S):
+    # Through a workspace, the O-proj and FFN2 Linears at M <= 8192 normalise
+    # their rows inside the GEMM kernel (the last workgroup of each M-tile,
+    # counted in on per-tile arrival counters).  That must equal the residual
+    # GEMM followed by the LayerNorm pass (the standalone launcher's path) bit
+    # for bit, call after call (the counters are re-armed by the kernel).
+    from bbh import engine
+
+    torch = torch_cuda
+    rng = np.random.default_rng(B * 1000 + S)
+    M = B * S
+    p = "encoder.layer.2."
+    w = {k[len(p):]: to_dev(torch, v.astype(np.float16)) for k, v in weights32.items()
+         if k.startswith(p)}
+    hid = to_dev(torch, _h(rng, (M, 384)))
+    mask = to_dev(torch, (rng.random((B, S)) < 0.8).astype(np.int32))
+    # FFN block: FFN1 + GELU, then FFN2 + residual + LayerNorm
+    inter = torch.empty((M, 1536), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(hid, w["intermediate.dense.weight"], inter, M, 1536, 384,
+                         bias=w["intermediate.dense.bias"], gelu=True)
+    want = torch.empty_like(hid)
+    engine.launch_linear_residual_layernorm(inter, w["output.dense.weight"], w["output.dense.bias"],
+                                            hid, w["output.LayerNorm.weight"],
+                                            w["output.LayerNorm.bias"], want, M, 1536)
+    for rep in range(3):
+        got = torch.empty_like(hid)
+        engine.ffn_block(ws, model, 2, hid, got, B, S)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (rep, (got.float() - want.float()).abs().max().item())
+    # attention block: QKV, attention, O-proj + residual + LayerNorm
+    qkv_w = torch.cat([w[f"attention.self.{n}.weight"] for n in ("query", "key", "value")])
+    qkv_b = torch.cat([w[f"attention.self.{n}.bias"] for n in ("query", "key", "value")])
+    qkv = torch.empty((M, 1152), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(hid, qkv_w, qkv, M, 1152, 384, bias=qkv_b)
+    ctx = torch.empty_like(hid)
+    engine.launch_attention(qkv, mask, ctx, B, S)
+    want_a = torch.empty_like(hid)
+    engine.launch_linear_residual_layernorm(ctx, w["attention.output.dense.weight"],
+                                            w["attention.output.dense.bias"], hid,
+                                            w["attention.output.LayerNorm.weight"],
+                                            w["attention.output.LayerNorm.bias"], want_a, M, 384)
+    for rep in range(2):
+        got_a = torch.empty_like(hid)
+        engine.attention_block(ws, model, 2, hid, mask, got_a, B, S)
+        torch.cuda.synchronize()
+        assert torch.equal(got_a, want_a), rep

@@ -54,6 +54,8 @@ SIGNATURES = {
     "bbh_workspace_hidden": (c_void_p, [c_void_p]),
     "bbh_embed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                           c_void_p]),
+    "bbh_embed_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                  c_void_p]),
     "bbh_encode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                            c_void_p]),
     "bbh_embed_graph_create": (c_int, [c_void_p] * 6 + [c_int, c_int, ctypes.POINTER(c_void_p)]),

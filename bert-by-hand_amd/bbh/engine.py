@@ -318,6 +318,24 @@ def bert_embed(ws: Workspace, w: Model, ids, types, mask, emb=None, batch=None, 
     return emb
 
 
+NOALLOC_MAX_ROWS = 8192  # BBH_NOALLOC_MAX_ROWS
+
+
+def bert_embed_noalloc(w: Model, ids, types, mask, emb=None, batch=None, seq=None, stream=None):
+    """bert_embed without a workspace (bbh_embed_noalloc): the library's own
+    device array holds the activations, so the call allocates nothing.  At
+    most NOALLOC_MAX_ROWS = batch * seq rows; calls overlapping on one GPU race."""
+    torch = _torch()
+    _check_i32(ids, types, mask)
+    batch = ids.shape[0] if batch is None else batch
+    seq = ids.shape[-1] if seq is None else seq
+    if emb is None:
+        emb = torch.empty((batch, HIDDEN), dtype=torch.float16, device=ids.device)
+    call("bbh_embed_noalloc", w.handle, _ptr(ids), _ptr(types), _ptr(mask), _ptr(emb), batch, seq,
+         _stream(stream))
+    return emb
+
+
 def bert_encode(ws: Workspace, w: Model, ids, types, mask, out=None, batch=None, seq=None,
                 stream=None):
     torch = _torch()

@@ -22,6 +22,7 @@
 #include <string>
 #include <algorithm>
 #include <map>
+#include <mutex>
 #include <vector>
 
 #include "../../include/bbh.h"
@@ -805,6 +806,79 @@ bbh_status bbh_embed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
   const hipStream_t s = S(stream);
   BBH_TRY(run_encode(ws, m, ids, types, mask, ws->attn_out, batch, seq, s));
   return check_launch(bbh::pool_normalize(ws->attn_out, mask, static_cast<f16*>(emb), batch, seq, s),
+                      "pool+normalize");
+}
+
+// ---- bbh_embed without a workspace ------------------------------------------
+// The forward's activations in a file-scope device array instead of a
+// workspace: BBH_NOALLOC_MAX_ROWS rows of the same six buffers (8,448 bytes a
+// row; 69.2 MB), which every GPU the library runs on holds until the process
+// ends.  Host code never names the array in a kernel argument or copy: its
+// address on each device comes from hipGetSymbolAddress, taken once per
+// device with that device current (the entry point's first call there).
+namespace {
+constexpr size_t kScratchRowBytes =
+    (3 * (size_t)BBH_HIDDEN + BBH_FFN_DIM + 4 * (size_t)BBH_HIDDEN) * sizeof(f16);
+constexpr size_t kScratchBytes = (size_t)BBH_NOALLOC_MAX_ROWS * kScratchRowBytes;
+static_assert(BBH_NOALLOC_MAX_ROWS % 64 == 0, "each buffer stays 256-byte aligned");
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once taken
+
+// The current device's copy of the scratch array (taken on first use).
+bbh_status scratch_on_current_device(void** out) {
+  int dev = -1;
+  BBH_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(BBH_ERR_UNSUPPORTED, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    BBH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(BBH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BBH_OK;
+}
+}  // namespace
+
+bbh_status bbh_embed_noalloc(const bbh_model* m, const int32_t* ids, const int32_t* types,
+                             const int32_t* mask, void* emb, int batch, int seq,
+                             bbh_stream_t stream) {
+  if (!m || !ids || !types || !mask || !emb)
+    return fail(BBH_ERR_INVALID_ARG, "bbh_embed_noalloc: null argument");
+  if (!aligned(emb, 4)) return misaligned("bbh_embed_noalloc emb");
+  BBH_TRY(check_shape(nullptr, batch, seq));
+  if ((size_t)batch * seq > BBH_NOALLOC_MAX_ROWS)
+    return fail(BBH_ERR_CAPACITY, "bbh_embed_noalloc: batch*seq " +
+                                      std::to_string((size_t)batch * seq) + " exceeds " +
+                                      std::to_string(BBH_NOALLOC_MAX_ROWS) + " rows");
+  void* base = nullptr;
+  BBH_TRY(scratch_on_current_device(&base));
+  // A workspace view of the array: the buffers bbh_workspace_create lays out,
+  // sized for BBH_NOALLOC_MAX_ROWS rows.  Every buffer is written before it is
+  // read within one forward, so nothing needs clearing between calls.
+  bbh_workspace ws;
+  ws.max_batch = BBH_NOALLOC_MAX_ROWS / BBH_SEQ_ALIGN;
+  ws.max_seq = BBH_MAX_POSITION;
+  ws.rows = BBH_NOALLOC_MAX_ROWS;
+  ws.blob = nullptr;  // not owned
+  ws.bytes = kScratchBytes;
+  f16* p = static_cast<f16*>(base);
+  const size_t R = BBH_NOALLOC_MAX_ROWS, H = BBH_HIDDEN;
+  ws.qkv = p;
+  ws.inter = ws.qkv + R * 3 * H;
+  ws.ctx = ws.inter + R * BBH_FFN_DIM;
+  ws.attn_out = ws.ctx + R * H;
+  ws.ping = ws.attn_out + R * H;
+  ws.pong = ws.ping + R * H;
+  ws.sents = nullptr;  // padded forwards only
+  const hipStream_t s = S(stream);
+  BBH_TRY(run_encode(&ws, m, ids, types, mask, ws.attn_out, batch, seq, s));
+  return check_launch(bbh::pool_normalize(ws.attn_out, mask, static_cast<f16*>(emb), batch, seq, s),
                       "pool+normalize");
 }
 

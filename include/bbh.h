@@ -125,6 +125,21 @@ void *bbh_workspace_hidden(bbh_workspace *ws);
 bbh_status bbh_embed(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
                      const int32_t *types, const int32_t *mask, void *emb,
                      int batch, int seq, bbh_stream_t stream);
+/* No counterpart in the reference: bbh_embed for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as bbh_embed
+ * without the workspace: the forward's activations live in a device array of
+ * the library (BBH_NOALLOC_MAX_ROWS rows, 69.2 MB on each GPU it runs on,
+ * held until the process ends), so the call performs no allocation of any
+ * kind on the success path.  batch*seq above BBH_NOALLOC_MAX_ROWS fails with
+ * BBH_ERR_CAPACITY before anything is enqueued.  Every call on one GPU uses
+ * the same array: calls that overlap in time on one GPU (two streams, two
+ * threads) race and must be serialised by the caller.  The embeddings equal
+ * bbh_embed's bit for bit. */
+#define BBH_NOALLOC_MAX_ROWS 8192 /* batch 64 x seq 128 */
+bbh_status bbh_embed_noalloc(const bbh_model *m, const int32_t *ids, const int32_t *types,
+                             const int32_t *mask, void *emb, int batch, int seq,
+                             bbh_stream_t stream);
 /* bert_encode (src/model/forward.h:11-13, forward.cu:20-42): final hidden
  * states (batch*seq, 384) fp16 into out. */
 bbh_status bbh_encode(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,

@@ -257,6 +257,118 @@ def classify(engine, recs, steps):
     return rows
 
 
+def short_kernel(name):
+    """Readable kernel class of a rocprofv3 kernel name (mangled or demangled)."""
+    import re
+
+    n = name.replace("(anonymous namespace)::", "").replace("bbh::", "").replace(" ", "")
+    m = (re.search(r"gemm_kernel<Cfg<([\d,]+)>,(\d)>", n) or
+         re.search(r"gemm_kernelINS0_3CfgILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)"
+                   r"EEELi(\d)E", n))
+    if m:
+        g = m.groups()
+        cfg, epi = (g[0], g[1]) if len(g) == 2 else (",".join(g[:7]), g[7])
+        return f"gemm_kernel<Cfg<{cfg}>, {epi}>"
+    m = re.search(r"gemm_wres_kernel(?:<|ILi)(\d)", n)
+    if m:
+        return f"gemm_wres_kernel<{m.group(1)}>"
+    m = (re.search(r"attention_kernel<(\d+),(\d+),(\d+),(\w+)>", n) or
+         re.search(r"attention_kernelILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)E", n))
+    if m:
+        vl = {"0": "false", "1": "true"}.get(m.group(4), m.group(4))
+        return f"attention_kernel<{m.group(1)},{m.group(2)},{m.group(3)},{vl}>"
+    if "at6native" in n or n.startswith("at::") or "at::native" in n:
+        return "torch kernel (" + ("copy" if "copy" in n else "fill/elementwise") + ")"
+    m = re.search(r"GLOBAL__N_1\d+([A-Za-z_0-9]+?)E", n) or re.match(r"(?:void)?([A-Za-z_0-9]+)", n)
+    return m.group(1) if m else n[:60]
+
+
+def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None):
+    """Per (kernel class, grid size) means over the dispatches of rocprofv3
+    --pmc counter_collection CSVs, as a markdown table.  FETCH_SIZE and
+    WRITE_SIZE (KiB) are turned into bytes with the copy-calibration scales;
+    with a --kernel-trace CSV, the mean duration (dispatches on `stream` only,
+    if given) and the HBM rate (fetch + write) / duration are added."""
+    import csv
+
+    acc, counters = {}, []
+    for p in paths:
+        for r in csv.DictReader(open(p)):
+            key = (short_kernel(r["Kernel_Name"]), int(r["Grid_Size"]))
+            c = r["Counter_Name"]
+            if c not in counters:
+                counters.append(c)
+            d = acc.setdefault(key, {}).setdefault(c, {})
+            d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    dur = {}
+    if trace:
+        for r in csv.DictReader(open(trace)):
+            if stream is not None and r["Stream_Id"] != str(stream):
+                continue
+            g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            dur.setdefault((short_kernel(r["Kernel_Name"]), g), []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    mean = lambda v: sum(v) / len(v)  # noqa: E731
+    cols = [c for c in counters if c not in ("FETCH_SIZE", "WRITE_SIZE")]
+    head = ["kernel", "grid (work-items)", "dispatches"]
+    if trace:
+        head += ["mean us (trace)"]
+    head += ["HBM read MB", "HBM write MB"] + (["HBM GB/s"] if trace else []) + cols
+    lines = ["| " + " | ".join(head) + " |", "|---|" + "---:|" * (len(head) - 1)]
+    rows = []
+    for (k, g), d in sorted(acc.items()):
+        n = max(len(v) for v in d.values())
+        rd = mean(d["FETCH_SIZE"].values()) * 1024 * fetch_scale if "FETCH_SIZE" in d else None
+        wr = mean(d["WRITE_SIZE"].values()) * 1024 * write_scale if "WRITE_SIZE" in d else None
+        us = mean(dur[(k, g)]) if (k, g) in dur else None
+        cells = [f"`{k}`", f"{g:,}", str(n)]
+        if trace:
+            cells.append(f"{us:.2f}" if us else "")
+        cells += [f"{rd / 1e6:.2f}" if rd is not None else "", f"{wr / 1e6:.2f}" if wr is not None else ""]
+        if trace:
+            cells.append(f"{(rd + wr) / (us * 1e-6) / 1e9:,.0f}" if us and rd is not None and wr is not None
+                         else "")
+        cells += [f"{mean(d[c].values()):,.2f}" if c in d else "" for c in cols]
+        lines.append("| " + " | ".join(cells) + " |")
+        rows.append({"kernel": k, "grid": g, "dispatches": n, "us": us, "read": rd, "write": wr})
+    return "\n".join(lines), rows
+
+
+def run_cfg5(torch, engine, synth, model, ws):
+    """batch 256 x seq 512 through bert_embed, each encoder GEMM
+    at M = 131072 on its own (fraction of the fp16 dense MFMA peak), and the
+    same batch through bbh_embed_packed (valid tokens only)."""
+    buf = gemm_buffers(torch, 131072)
+    ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())
+    emb5 = torch.empty((256, 384), dtype=torch.float16, device="cuda")
+    ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb5), 10,
+               warmup=2)
+    gemm_ms, gemm_flops = 0.0, 0.0
+    gem = {}
+    for name, N, K, epi in LAYER_GEMMS:
+        fn = gemm_runner(torch, engine, model, 131072, N, K, epi, buf)
+        t = timed(torch, fn, 10, warmup=2)
+        f = 2.0 * 131072 * N * K
+        gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
+        gemm_ms += t
+        gemm_flops += f
+    del buf
+    # lengths uniform in [256, 512]: about 3/4 of the padded rows are valid
+    pk5 = engine.PackedBatches([synth.long_batch()])
+    pool5 = engine.Pool(1, 256, 512)
+    ms_p5 = timed(torch, lambda: engine.embed_packed(pool5, model, pk5, emb=emb5), 10, warmup=2)
+    pool5.close()
+    res = {
+        "sentences_per_s": round(256 / (ms / 1e3), 1), "ms_per_forward": round(ms, 3),
+        "packed_sentences_per_s": round(256 / (ms_p5 / 1e3), 1),
+        "packed_valid_tokens": int(pk5.lengths.sum()),
+        "tflops": round(synth.flops_per_forward(256, 512) / (ms / 1e3) / 1e12, 2),
+        "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
+        "per_gemm_frac": gem}
+    log("cfg5", res)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,7 +379,24 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only time a device-to-device copy of BYTES (the calibration kernel "
                          "for the HBM byte counters, and the practical copy bandwidth)")
+    ap.add_argument("--only", choices=["varlen", "cfg5"], default=None,
+                    help="only this workload, without the event-timed roofline pass (for "
+                         "rocprofv3 counter runs); prints its dict")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV", default=None,
+                    help="no GPU work: summarise rocprofv3 --pmc counter_collection CSVs per "
+                         "kernel class and grid size as a markdown table")
+    ap.add_argument("--trace", metavar="CSV", default=None,
+                    help="with --pmc-summary: a rocprofv3 kernel_trace CSV for mean durations")
+    ap.add_argument("--trace-stream", default=None,
+                    help="with --trace: only dispatches of this Stream_Id")
+    ap.add_argument("--scales", nargs=2, type=float, default=(1.0, 1.0), metavar=("FETCH", "WRITE"),
+                    help="with --pmc-summary: bytes per reported FETCH_SIZE / WRITE_SIZE byte, "
+                         "from the same counters on the --copy-probe copy")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary, args.trace, args.scales[0], args.scales[1],
+                          args.trace_stream)[0])
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; the embedding path is pure data "
@@ -292,6 +421,25 @@ def main():
         return
     weights = synth.make_weights(0)
     model = engine.Model.from_weights(weights)
+    if args.only == "varlen":  # the default workload's pass alone
+        batches = synth.varlen_mix()
+        pk = engine.PackedBatches([b[:3] for b in batches])
+        emb_all = torch.empty((pk.rows, 384), dtype=torch.float16, device="cuda")
+        pool = engine.Pool(EACH_STREAMS, 64, 64)
+        ms, _ = pass_timer(torch, lambda: engine.embed_each(pool, model, pk, emb=emb_all),
+                           args.steps, args.warmup)
+        pool.close()
+        model.close()
+        print(json.dumps({"workload": "varlen per-batch pass", "streams": EACH_STREAMS,
+                          "ms_per_pass": round(ms, 4), "sentences_per_s": round(2000 / (ms / 1e3), 1)}),
+              flush=True)
+        return
+    if args.only == "cfg5":
+        ws = engine.Workspace(256, 512)
+        print(json.dumps(run_cfg5(torch, engine, synth, model, ws)), flush=True)
+        ws.close()
+        model.close()
+        return
 
     # ---- default workload: varlen mix, one bert_embed per batch ------------
     # The 32 consecutive batches of 64, each at its own padded round16 length,
@@ -449,38 +597,8 @@ def main():
                         "graph_sentences_per_s": round(64 / (ms_g / 1e3), 1),
                         "graph_ms_per_sentence": round(ms_g / 64, 6)}
             log(tag, out[tag])
-        # ---- batch 256 x seq 512 ---------------------------------
-        buf = gemm_buffers(torch, 131072)
-        ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())
-        emb5 = torch.empty((256, 384), dtype=torch.float16, device="cuda")
-        ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb5), 10,
-                   warmup=2)
-        gemm_ms, gemm_flops = 0.0, 0.0
-        gem = {}
-        for name, N, K, epi in LAYER_GEMMS:
-            fn = gemm_runner(torch, engine, model, 131072, N, K, epi, buf)
-            t = timed(torch, fn, 10, warmup=2)
-            f = 2.0 * 131072 * N * K
-            gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
-            gemm_ms += t
-            gemm_flops += f
-        del buf
-        # the same batch through bbh_embed_packed (valid tokens only: lengths
-        # uniform in [256, 512], so about 3/4 of the padded rows)
-        pk5 = engine.PackedBatches([synth.long_batch()])
-        pool5 = engine.Pool(1, 256, 512)
-        ms_p5 = timed(torch, lambda: engine.embed_packed(pool5, model, pk5, emb=emb5), 10,
-                      warmup=2)
-        pool5.close()
+        out["cfg5_b256_s512"] = run_cfg5(torch, engine, synth, model, ws)
         ws.close()
-        out["cfg5_b256_s512"] = {
-            "sentences_per_s": round(256 / (ms / 1e3), 1), "ms_per_forward": round(ms, 3),
-            "packed_sentences_per_s": round(256 / (ms_p5 / 1e3), 1),
-            "packed_valid_tokens": int(pk5.lengths.sum()),
-            "tflops": round(synth.flops_per_forward(256, 512) / (ms / 1e3) / 1e12, 2),
-            "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
-            "per_gemm_frac": gem}
-        log("cfg5", out["cfg5_b256_s512"])
         out["tokenizer"] = tokenizer_rate(engine, synth)
         log("tokenizer", out["tokenizer"])
 

@@ -409,13 +409,15 @@ def test_pool_normalize(torch_cuda, B, S):
         assert np.all(got[2] == 0.0)
 
 
-@pytest.mark.parametrize("B,S", [(1, 16), (64, 16), (31, 48), (64, 48), (64, 64), (96, 64), (64, 128)])
+@pytest.mark.parametrize("B,S", [(1, 16), (64, 16), (5, 32), (31, 48), (64, 48), (64, 64), (96, 64),
+                                 (128, 64), (64, 128)])
 def test_workspace_residual_layernorm_equals_two_pass(torch_cuda, ws, model, weights32, B, S):
-    # Through a workspace, the O-proj and FFN2 Linears at M <= 8192 normalise
-    # their rows inside the GEMM kernel (the last workgroup of each M-tile,
-    # counted in on per-tile arrival counters).  That must equal the residual
-    # GEMM followed by the LayerNorm pass (the standalone launcher's path) bit
-    # for bit, call after call (the counters are re-armed by the kernel).
+    # The workspace blocks (bbh_ffn_block, bbh_attention_block) against their
+    # kernels launched one by one through the standalone launchers (Linear,
+    # attention, Linear + residual + LayerNorm): equal bit for bit, call after
+    # call, at every M regime of a batch-64 forward (and 8192 rows, the last
+    # with a separate LayerNorm pass); masks with holes, a fully masked
+    # sentence and a one-key sentence included.
     from bbh import engine
 
     torch = torch_cuda
@@ -425,7 +427,12 @@ def test_workspace_residual_layernorm_equals_two_pass(torch_cuda, ws, model, wei
     w = {k[len(p):]: to_dev(torch, v.astype(np.float16)) for k, v in weights32.items()
          if k.startswith(p)}
     hid = to_dev(torch, _h(rng, (M, 384)))
-    mask = to_dev(torch, (rng.random((B, S)) < 0.8).astype(np.int32))
+    m = (rng.random((B, S)) < 0.8).astype(np.int32)
+    m[0, :] = 1
+    if B > 2:
+        m[1, :] = 0  # every key masked: zero context
+        m[2, 1:] = 0  # one key
+    mask = to_dev(torch, m)
     # FFN block: FFN1 + GELU, then FFN2 + residual + LayerNorm
     inter = torch.empty((M, 1536), dtype=torch.float16, device="cuda")
     engine.launch_matmul(hid, w["intermediate.dense.weight"], inter, M, 1536, 384,

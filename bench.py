@@ -215,26 +215,37 @@ def launch_work(r):
 
 
 def kernel_name(engine, op, tile, fused):
-    if op == "attention":
-        return "attention_kernel"
-    if op == "embed":
-        return "embedding_ln_kernel"
-    if op == "pool":
-        return "pool_normalize_kernel"
-    if op == "layernorm":
-        return "ln384_kernel"
+    """(display name, class name as short_kernel() writes it) of a launch record."""
+    row = {"attention": "attention_kernel", "embed": "embedding_ln_kernel",
+           "pool": "pool_normalize_kernel", "layernorm": "ln384_kernel"}
+    if op in row:
+        return row[op], row[op]
     epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else "2 (bias+residual)")
     tname = engine.gemm_tile_name(tile)
-    return (f"gemm_wres_kernel<{epi}>" if tname.startswith("WRes") else
-            f"gemm_kernel<{tname}, {epi}>")
+    if tname.startswith("WRes"):
+        return f"gemm_wres_kernel<{epi}>", f"gemm_wres_kernel<{epi[0]}>"
+    return f"gemm_kernel<{tname}, {epi}>", f"gemm_kernel<{tname}, {epi[0]}>"
+
+
+def gemm_grid_items(tile_name, M, N):
+    """Work-items of a tiled-GEMM launch (the launcher's grid: N/BN column
+    tiles x 8 XCDs x ceil(M-tiles / 8), 64*WM*WN threads), as rocprofv3
+    reports Grid_Size; None for other kernels."""
+    import re
+
+    m = re.match(r"Cfg<(\d+),(\d+),(\d+),(\d+),", tile_name)
+    if not m:
+        return None
+    bm, bn, wm, wn = (int(x) for x in m.groups())
+    return (N // bn) * 8 * ((-(-M // bm) + 7) // 8) * 64 * wm * wn
 
 
 def classify(engine, recs, steps):
-    """Launch records -> classes keyed (op, tile, fused): summed ms, count, M
-    values, algorithmic FLOPs and bytes."""
+    """Launch records -> classes keyed (op, tile, fused, M): summed ms, count,
+    algorithmic FLOPs and bytes, sorted by summed time."""
     classes = {}
     for r in recs:
-        key = (r["op"], r["tile"], r["fused_ln"])
+        key = (r["op"], r["tile"], r["fused_ln"], r["m"])
         c = classes.setdefault(key, {"ms": 0.0, "n": 0, "flops": 0.0, "bytes": 0.0, "m": set()})
         f, b = launch_work(r)
         c["ms"] += r["ms"]
@@ -244,9 +255,12 @@ def classify(engine, recs, steps):
         c["bytes"] += b
     total = sum(c["ms"] for c in classes.values())
     rows = []
-    for (op, tile, fused), c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
+    for (op, tile, fused, m), c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
         avg_s = c["ms"] / c["n"] / 1e3
-        rows.append({"kernel": kernel_name(engine, op, tile, fused), "op": op, "m": sorted(c["m"]),
+        name, cls = kernel_name(engine, op, tile, fused)
+        n_out = {"qkv": 1152, "ffn1_gelu": 1536}.get(op, 384)
+        grid = gemm_grid_items(engine.gemm_tile_name(tile), m, n_out) if tile >= 0 else None
+        rows.append({"kernel": name, "class": cls, "op": op, "m": m, "grid_items": grid,
                      "launches_per_step": round(c["n"] / steps, 2),
                      "avg_launch_us": round(avg_s * 1e6, 2),
                      "tflops": round(c["flops"] / c["n"] / avg_s / 1e12, 1),
@@ -392,10 +406,25 @@ def main():
     ap.add_argument("--scales", nargs=2, type=float, default=(1.0, 1.0), metavar=("FETCH", "WRITE"),
                     help="with --pmc-summary: bytes per reported FETCH_SIZE / WRITE_SIZE byte, "
                          "from the same counters on the --copy-probe copy")
+    ap.add_argument("--traffic-json", metavar="OUT", default=None,
+                    help="with --pmc-summary: also write each kernel class's HBM bytes per "
+                         "dispatch (fetch + write, dispatch-weighted over its grids) to OUT")
     args = ap.parse_args()
     if args.pmc_summary:
-        print(pmc_summary(args.pmc_summary, args.trace, args.scales[0], args.scales[1],
-                          args.trace_stream)[0])
+        table, rows = pmc_summary(args.pmc_summary, args.trace, args.scales[0], args.scales[1],
+                                  args.trace_stream)
+        print(table)
+        if args.traffic_json:
+            cls = {}
+            for r in rows:
+                if r["read"] is None or r["write"] is None:
+                    continue
+                c = cls.setdefault(r["kernel"], {})
+                c[str(r["grid"])] = round(r["read"] + r["write"])
+            json.dump({"source": " ".join(sys.argv), "fetch_scale": args.scales[0],
+                       "write_scale": args.scales[1],
+                       "kernels": [{"class": k, "grid_bytes": v} for k, v in sorted(cls.items())]},
+                      open(args.traffic_json, "w"), indent=1)
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -512,14 +541,15 @@ def main():
     peak = PEAK_FP16_DENSE / 1e12 if gemm else PEAK_HBM / 1e9
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
-    if os.path.exists(tfile):
+    if os.path.exists(tfile):  # HBM bytes per dispatch of each class in a --pmc run of this pass
         for t in json.load(open(tfile)).get("kernels", []):
-            if t.get("kernel") == dom["kernel"] and t.get("op") == dom["op"] and t.get("m") == dom["m"]:
-                traffic = t["traffic_bytes_per_launch"]
+            g = str(dom["grid_items"])
+            if t.get("class") == dom["class"] and g in t.get("grid_bytes", {}):
+                traffic = t["grid_bytes"][g]
     out["roofline"] = {
         "bound": "mfma" if gemm else "hbm", "achieved": ach, "peak": peak,
         "unit": "TFLOP/s" if gemm else "GB/s", "frac": round(ach / peak, 4), "traffic": traffic,
-        "kernel": dom["kernel"], "op": dom["op"], "m": dom["m"],
+        "kernel": dom["kernel"], "op": dom["op"], "m": dom["m"], "grid_items": dom["grid_items"],
         "launches_per_step": dom["launches_per_step"], "avg_launch_us": dom["avg_launch_us"],
         "algorithmic_flops_per_launch": dom["algorithmic_flops_per_launch"],
         "algorithmic_bytes_per_launch": dom["algorithmic_bytes_per_launch"],

@@ -208,7 +208,10 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
  * those of bbh_embed on that batch.  Batch i goes, in batch order, to the
  * stream with the fewest rows so far; the call orders itself after prior
  * work on `stream`, makes later work on `stream` wait for all batches, and
- * returns without a host sync. */
+ * returns without a host sync.  With more than one stream in use (and op
+ * timing off) each stream's launches are enqueued by a host thread of its
+ * own, started and joined inside the call; the caller's current HIP device
+ * is made current in those threads. */
 bbh_status bbh_embed_each(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
                           const int32_t *types, const int32_t *mask,
                           const int64_t *tok_offsets, const int *batch_sizes, const int *seqs,

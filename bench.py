@@ -209,6 +209,8 @@ def launch_work(r):
         return 0.0, M * N * (768.0 + 4) + M * 768.0
     if op == "layernorm":  # rows read and written in place, gamma/beta
         return 0.0, M * 1536.0 + 1536
+    if op == "ffn":  # (M, 384, 1536): both Linears; X in (also the residual), out, weights
+        return 4.0 * M * N * K, (2 * M * N + 2 * N * K + K + 3 * N) * 2.0
     flops = 2.0 * M * N * K
     byts = (M * K + N * K + M * N + N) * 2.0
     if op in ("o_proj_ln", "ffn2_ln"):
@@ -219,7 +221,8 @@ def launch_work(r):
 def kernel_name(engine, op, tile, fused):
     """(display name, class name as short_kernel() writes it) of a launch record."""
     row = {"attention": "attention_kernel", "embed": "embedding_ln_kernel",
-           "pool": "pool_normalize_kernel", "layernorm": "ln384_kernel"}
+           "pool": "pool_normalize_kernel", "layernorm": "ln384_kernel",
+           "ffn": "ffn_fused_kernel"}
     if op in row:
         return row[op], row[op]
     epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else "2 (bias+residual)")

@@ -171,7 +171,7 @@ class Pool:
         call("bbh_pool_timing", self.handle, capacity)
 
     OPS = {1: "qkv", 2: "attention", 3: "o_proj_ln", 4: "ffn1_gelu", 5: "ffn2_ln", 6: "embed",
-           7: "pool", 8: "layernorm"}
+           7: "pool", 8: "layernorm", 9: "ffn"}
 
     def timing_read(self):
         """The recorded launches: dicts of op, tile, fused_ln, m, n, k, ms."""

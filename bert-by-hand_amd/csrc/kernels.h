@@ -44,6 +44,15 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
 hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,
                          int M, int K, hipStream_t s);
 
+// The whole feed-forward block in one kernel for M >= ffn_fused_ok's bound:
+// out(M,384) = LN(GELU(X . W1^T + b1) . W2^T + b2 + X) * gamma + beta, with the
+// intermediate kept on chip; the arithmetic of gemm(.., kGelu) followed by
+// gemm_residual_ln (equal but for rare fp16 rounding midpoints).  out may
+// alias X.  X, W1, W2, out 16-byte aligned; the vectors 8-byte aligned.
+bool ffn_fused_ok(int M);
+hipError_t ffn_fused(const f16* X, const f16* W1, const f16* b1, const f16* W2, const f16* b2,
+                     const f16* gamma, const f16* beta, f16* out, int M, float eps, hipStream_t s);
+
 // Fused masked attention from the QKV activations (row stride 3*heads*32).
 hipError_t attention(const f16* qkv, const int32_t* mask, f16* merged, int batch,
                      int heads, int seq, float scale, hipStream_t s);

@@ -265,7 +265,9 @@ typedef enum bbh_op {
   BBH_OP_FFN2_LN = 5,   /* output Linear + residual (+ LayerNorm when fused) */
   BBH_OP_EMBED = 6,     /* embedding gather + embedding LayerNorm */
   BBH_OP_POOL = 7,      /* masked mean pool + L2 normalize */
-  BBH_OP_LAYERNORM = 8  /* residual LayerNorm pass after an unfused O-proj / FFN2 */
+  BBH_OP_LAYERNORM = 8, /* residual LayerNorm pass after an unfused O-proj / FFN2 */
+  BBH_OP_FFN = 9        /* the whole FFN block (intermediate Linear + GELU, output Linear +
+                           residual + LayerNorm) in one kernel, at large M */
 } bbh_op;
 typedef struct bbh_launch_time {
   int op;       /* bbh_op */
@@ -273,7 +275,7 @@ typedef struct bbh_launch_time {
   int fused_ln; /* O-proj / FFN2: 1 when the LayerNorm runs inside the GEMM kernel, 0 when it
                    follows as its own BBH_OP_LAYERNORM record */
   int m, n, k;  /* GEMM (M, N, K); attention (batch, seq, heads); embed / pool / LayerNorm
-                   (rows or sentences, seq or 384, 0) */
+                   (rows or sentences, seq or 384, 0); FFN (M, 384, 1536) */
   float ms;     /* time between the pair of events */
 } bbh_launch_time;
 bbh_status bbh_pool_timing(bbh_pool *pool, int capacity);

@@ -409,6 +409,56 @@ def test_pool_normalize(torch_cuda, B, S):
         assert np.all(got[2] == 0.0)
 
 
+@pytest.mark.parametrize("B,S", [(4097, 16), (192, 512), (256, 512)])
+def test_ffn_one_kernel_equals_two_kernels(torch_cuda, ws, model, weights32, weights16, B, S):
+    # From 65536 rows bbh_ffn_block runs the FFN as one kernel (intermediate
+    # kept on chip).  Against the intermediate Linear + GELU and the output
+    # Linear + residual + LayerNorm launched one by one through the standalone
+    # launchers, call after call: a ragged last 128-row block (4097 x 16 =
+    # 65552 rows), three and four row blocks per workgroup (98304, 131072
+    # rows).  Same arithmetic, so the outputs agree except where an fp16
+    # rounding falls on a midpoint: at most one fp16 step, on at most 2e-5 of
+    # the elements.  Then against the fp32 oracle on rows at the start, middle
+    # and end.  (The forward runs the kernel in place on its last layer:
+    # covered end to end by the cfg5 tests.)
+    from bbh import engine
+
+    torch = torch_cuda
+    rng = np.random.default_rng(B * 7 + S)
+    M = B * S
+    p = "encoder.layer.4."
+    w = {k[len(p):]: to_dev(torch, v.astype(np.float16)) for k, v in weights32.items()
+         if k.startswith(p)}
+    hid = to_dev(torch, _h(rng, (M, 384)))
+    inter = torch.empty((M, 1536), dtype=torch.float16, device="cuda")
+    engine.launch_matmul(hid, w["intermediate.dense.weight"], inter, M, 1536, 384,
+                         bias=w["intermediate.dense.bias"], gelu=True)
+    want = torch.empty_like(hid)
+    engine.launch_linear_residual_layernorm(inter, w["output.dense.weight"], w["output.dense.bias"],
+                                            hid, w["output.LayerNorm.weight"],
+                                            w["output.LayerNorm.bias"], want, M, 1536)
+    del inter
+    wn = _np(want)
+    step = np.spacing(np.abs(wn).astype(np.float16)).astype(np.float32)  # one fp16 step
+    first = None
+    for rep in range(2):
+        got = torch.empty_like(hid)
+        engine.ffn_block(ws, model, 4, hid, got, B, S)
+        torch.cuda.synchronize()
+        g = _np(got)
+        diff = g != wn
+        assert diff.mean() <= 2e-5, (rep, int(diff.sum()))
+        assert np.all(np.abs(g - wn)[diff] <= step[diff]), rep
+        if first is None:
+            first = g
+        else:
+            assert np.array_equal(g, first)  # deterministic call after call
+    rows = np.r_[0:40, M // 2 - 20:M // 2 + 20, M - 40:M]
+    x = _np(hid)[rows]
+    ref = O.ffn_block(x.reshape(1, -1, 384), O._layer(weights16, 4)).reshape(-1, 384)
+    assert np.abs(_np(got)[rows] - ref).max() <= TOL
+
+
 @pytest.mark.parametrize("B,S", [(1, 16), (64, 16), (5, 32), (31, 48), (64, 48), (64, 64), (96, 64),
                                  (128, 64), (64, 128)])
 def test_workspace_residual_layernorm_equals_two_pass(torch_cuda, ws, model, weights32, B, S):

@@ -354,23 +354,35 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
 
 
 def run_cfg5(torch, engine, synth, model, ws):
-    """batch 256 x seq 512 through bert_embed, each encoder GEMM
-    at M = 131072 on its own (fraction of the fp16 dense MFMA peak), and the
-    same batch through bbh_embed_packed (valid tokens only)."""
-    buf = gemm_buffers(torch, 131072)
+    """batch 256 x seq 512 through bert_embed; the encoder layer's
+    GEMM launches at M = 131072 as the forward makes them (QKV, O-proj +
+    LayerNorm, and the FFN block, which from 65536 rows is one kernel for both
+    of its Linears), each timed on its own: their FLOPs over their summed time
+    is the fraction of the fp16 dense MFMA peak; the two FFN Linears as
+    separate kernels are reported beside it.  Then the same batch through
+    bbh_embed_packed (valid tokens only)."""
+    M = 131072
+    buf = gemm_buffers(torch, M)
     ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.long_batch())
     emb5 = torch.empty((256, 384), dtype=torch.float16, device="cuda")
     ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb5), 10,
                warmup=2)
-    gemm_ms, gemm_flops = 0.0, 0.0
-    gem = {}
+    gem, sep = {}, {}
     for name, N, K, epi in LAYER_GEMMS:
-        fn = gemm_runner(torch, engine, model, 131072, N, K, epi, buf)
+        fn = gemm_runner(torch, engine, model, M, N, K, epi, buf)
         t = timed(torch, fn, 10, warmup=2)
-        f = 2.0 * 131072 * N * K
+        f = 2.0 * M * N * K
+        sep[name] = (t, f)
         gem[name] = round(f / (t / 1e3) / PEAK_FP16_DENSE, 4)
-        gemm_ms += t
-        gemm_flops += f
+    # the FFN block as the forward runs it (layer 0 of the model, synthetic input rows)
+    hid = buf["R"][: M * 384].view(M, 384)
+    out = buf["C"][: M * 384].view(M, 384)
+    t_ffn = timed(torch, lambda: engine.ffn_block(ws, model, 0, hid, out, 256, 512), 10, warmup=2)
+    f_ffn = sep["ffn1_gelu"][1] + sep["ffn2_ln"][1]
+    gem["ffn_block"] = round(f_ffn / (t_ffn / 1e3) / PEAK_FP16_DENSE, 4)
+    gemm_ms = sep["qkv"][0] + sep["o_proj_ln"][0] + t_ffn
+    gemm_flops = sep["qkv"][1] + sep["o_proj_ln"][1] + f_ffn
+    two = sum(t for t, _ in sep.values())
     del buf
     # lengths uniform in [256, 512]: about 3/4 of the padded rows are valid
     pk5 = engine.PackedBatches([synth.long_batch()])
@@ -383,6 +395,8 @@ def run_cfg5(torch, engine, synth, model, ws):
         "packed_valid_tokens": int(pk5.lengths.sum()),
         "tflops": round(synth.flops_per_forward(256, 512) / (ms / 1e3) / 1e12, 2),
         "fused_gemms_frac_of_fp16_peak": round(gemm_flops / (gemm_ms / 1e3) / PEAK_FP16_DENSE, 4),
+        "fused_gemms_frac_ffn_as_two_kernels": round(gemm_flops / (two / 1e3) / PEAK_FP16_DENSE, 4),
+        "layer_gemm_us": round(gemm_ms * 1e3, 1),
         "per_gemm_frac": gem}
     log("cfg5", res)
     return res

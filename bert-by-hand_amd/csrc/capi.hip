@@ -353,7 +353,9 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
 bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
                         f16* out, int M, hipStream_t s, OpTimer* t = nullptr) {
   const int H = BBH_HIDDEN, F = BBH_FFN_DIM;
-  if (bbh::ffn_fused_ok(M))
+  // One kernel for the block at large M; it moves rows in 16-byte pieces
+  // (the GEMM path falls back to its any-alignment kernel instead).
+  if (bbh::ffn_fused_ok(M) && aligned(hidden, 16) && aligned(out, 16))
     return timed_op(t, s, {BBH_OP_FFN, -1, 1, M, H, F, 0.f}, [&] {
       return check_launch(bbh::ffn_fused(hidden, L.f1_w, L.f1_b, L.f2_w, L.f2_b, L.ln2_g, L.ln2_b,
                                          out, M, BBH_LAYER_NORM_EPS, s),

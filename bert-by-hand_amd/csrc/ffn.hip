@@ -19,11 +19,11 @@
 //    accumulator (32 x 192 fp32, 96 VGPRs each), add H . W2[:, c]^T one chunk
 //    behind the producer, and at the end of the block add bias and residual
 //    and run the LayerNorm, exchanging row partial sums through LDS.
-// On MI355X one wavefront's VALU work barely overlaps its own MFMAs but
-// overlaps another wavefront's on the same SIMD almost fully, so the GELU of
-// chunk c runs under the consumers' MFMAs of chunk c - 1.  Three wavefronts
-// per SIMD leave each 168 registers; the kernel uses no AGPRs, so all of them
-// are VGPRs (a function with AGPRs gets half its budget in each file).
+// The GELU of chunk c runs beside the consumers' MFMAs of chunk c - 1 on the
+// same SIMD (MFMA and VALU work of different wavefronts overlap).  Three
+// wavefronts per SIMD leave each 168 registers; the kernel uses no AGPRs, so
+// all of them are VGPRs (a function with AGPRs gets half its budget in each
+// file).
 //
 // Phases.  Phase k: the producer makes chunk k, the consumers consume chunk
 // k - 1; one workgroup barrier ends each phase.  Weights stream in pieces of
@@ -44,10 +44,16 @@
 // 16592 rows, one fp16 step apart, each kernel as often the nearer to a
 // float64 evaluation).
 //
-// Bound: LDS.  Every MFMA reads a 1 KB weight fragment from LDS (the other
-// operand is in registers), which alone is ~128 B/clk per CU at the MFMA
-// rate, the LDS read rate measured on MI355X; the 48 KB of global_load_lds
-// writes per phase come on top.
+// Bound: the producer's chain.  Timestamps of one workgroup at M = 131,072
+// put a phase at ~3,450 cycles: the producer spends ~1,140 on its 24 MFMAs
+// (one dependent chain, sharing the matrix core with the consumers' 24),
+// ~1,500 on the GELU and ~300 handing H over, then reaches the barrier; the
+// consumers spend 700-1,250 cycles issuing their copies (48 KB a phase at
+// ~64 B/clk per CU through the texture path), ~1,100 on their MFMAs, and
+// wait.  The matrix core is busy ~45% of the phase.  LDS traffic, ~264 KB a
+// phase per CU (every MFMA reads a 1 KB weight fragment; the other operand
+// is in registers), stays under what the LDS sustains with two or more
+// wavefronts per SIMD (~220-260 B/clk per CU).
 
 #include "kernels.h"
 #include "pipe.h"

@@ -987,16 +987,19 @@ const char* tile_name(int id) {
 // (1536, 384) FFN1, (384, 384) O-proj and (384, 1536) FFN2.  QKV and FFN1 at
 // large M run on the weight-resident kernel instead (wres_ok).  Small M wants
 // many small tiles (latency, CU coverage); large M wants big tiles (L2 and
-// LDS traffic per MFMA).
+// LDS traffic per MFMA).  FFN2 from 2049 to 4096 rows takes the copy-ring
+// 64x64 tile (0), not the register-staged one (26): equal alone, 1.8% ahead
+// in the per-batch pass on three streams, where its L2 -> LDS copies do not
+// go through VGPRs (~57 against ~15-18 B/clk per CU).
 int pick_plain(int M, int N, int K) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
   if (M <= 2048)
     id = qkv ? 30 : ffn1 ? 0 : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? 26 : wide_k ? 26 : 0;
+    id = qkv ? 30 : ffn1 ? 26 : 0;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 26 : 0;
+    id = qkv ? 32 : ffn1 ? 30 : 0;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

@@ -302,6 +302,33 @@ def short_kernel(name):
     return m.group(1) if m else n[:60]
 
 
+def op_tags(rows, queue_col, grid):
+    """Dispatch_Id -> " [o_proj]" / " [ffn2]" for the residual GEMMs of
+    profiler rows.  O-proj and FFN2 can run the same kernel on the same grid
+    (e.g. the 64x64 copy-ring tile at 2049-4096 rows), so kernel name and grid
+    do not tell them apart; within one queue, an encoder layer runs O-proj
+    right after attention and FFN2 right after the GELU Linear (FFN1)."""
+    import re
+
+    seen, order = set(), []
+    for r in rows:  # counter CSVs hold one row per counter and dispatch
+        if r["Dispatch_Id"] not in seen:
+            seen.add(r["Dispatch_Id"])
+            order.append(r)
+    order.sort(key=lambda r: (r[queue_col], int(r["Dispatch_Id"])))
+    tags, prev = {}, {}
+    for r in order:
+        q, k = r[queue_col], short_kernel(r["Kernel_Name"])
+        p = prev.get(q)
+        if re.match(r"gemm_(kernel<.*, [23]>|wres_kernel<3>)$", k) and p:
+            if p.startswith("attention_kernel"):
+                tags[r["Dispatch_Id"]] = " [o_proj]"
+            elif re.match(r"gemm_(kernel<.*, 1>|wres_kernel<1>)$", p):
+                tags[r["Dispatch_Id"]] = " [ffn2]"
+        prev[q] = k
+    return tags
+
+
 def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None):
     """Per (kernel class, grid size) means over the dispatches of rocprofv3
     --pmc counter_collection CSVs, as a markdown table.  FETCH_SIZE and
@@ -312,8 +339,10 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
 
     acc, counters = {}, []
     for p in paths:
-        for r in csv.DictReader(open(p)):
-            key = (short_kernel(r["Kernel_Name"]), int(r["Grid_Size"]))
+        rows = list(csv.DictReader(open(p)))
+        tags = op_tags(rows, "Queue_Id", lambda r: int(r["Grid_Size"]))
+        for r in rows:
+            key = (short_kernel(r["Kernel_Name"]) + tags.get(r["Dispatch_Id"], ""), int(r["Grid_Size"]))
             c = r["Counter_Name"]
             if c not in counters:
                 counters.append(c)
@@ -321,12 +350,13 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
             d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
     dur = {}
     if trace:
-        for r in csv.DictReader(open(trace)):
-            if stream is not None and r["Stream_Id"] != str(stream):
-                continue
-            g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
-            dur.setdefault((short_kernel(r["Kernel_Name"]), g), []).append(
-                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        grid = lambda r: int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])  # noqa: E731
+        rows = [r for r in csv.DictReader(open(trace))
+                if stream is None or r["Stream_Id"] == str(stream)]
+        tags = op_tags(rows, "Stream_Id", grid)
+        for r in rows:
+            dur.setdefault((short_kernel(r["Kernel_Name"]) + tags.get(r["Dispatch_Id"], ""), grid(r)),
+                           []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     mean = lambda v: sum(v) / len(v)  # noqa: E731
     cols = [c for c in counters if c not in ("FETCH_SIZE", "WRITE_SIZE")]
     head = ["kernel", "grid (work-items)", "dispatches"]
@@ -351,6 +381,34 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
         lines.append("| " + " | ".join(cells) + " |")
         rows.append({"kernel": k, "grid": g, "dispatches": n, "us": us, "read": rd, "write": wr})
     return "\n".join(lines), rows
+
+
+def trace_summary(trace, stream):
+    """Per (kernel class, grid) of a rocprofv3 --kernel-trace CSV:
+    dispatches, mean duration on Stream_Id `stream` and on the other
+    streams, share of all kernel time; residual GEMMs tagged by op
+    (op_tags).  A markdown table, largest share first."""
+    import csv
+
+    rows = list(csv.DictReader(open(trace)))
+    grid = lambda r: int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])  # noqa: E731
+    tags = op_tags(rows, "Stream_Id", grid)
+    acc, total = {}, 0.0
+    for r in rows:
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        total += us
+        c = acc.setdefault((short_kernel(r["Kernel_Name"]) + tags.get(r["Dispatch_Id"], ""), grid(r)),
+                           {"n": 0, "sum": 0.0, "own": [], "other": []})
+        c["n"] += 1
+        c["sum"] += us
+        c["own" if r["Stream_Id"] == str(stream) else "other"].append(us)
+    mean = lambda v: f"{sum(v) / len(v):.2f}" if v else ""  # noqa: E731
+    lines = ["| kernel | grid (work-items) | dispatches | mean us, timing stream | "
+             "mean us, concurrent streams | % of kernel time |", "|---|---:|---:|---:|---:|---:|"]
+    for (k, g), c in sorted(acc.items(), key=lambda kv: -kv[1]["sum"]):
+        lines.append(f"| `{k}` | {g:,} | {c['n']} | {mean(c['own'])} | {mean(c['other'])} | "
+                     f"{100 * c['sum'] / total:.1f} |")
+    return "\n".join(lines)
 
 
 def run_cfg5(torch, engine, synth, model, ws):
@@ -420,6 +478,9 @@ def main():
                          "kernel class and grid size as a markdown table")
     ap.add_argument("--trace", metavar="CSV", default=None,
                     help="with --pmc-summary: a rocprofv3 kernel_trace CSV for mean durations")
+    ap.add_argument("--trace-summary", metavar="CSV", default=None,
+                    help="print per-kernel-class times of a rocprofv3 kernel_trace CSV "
+                         "(--trace-stream: the timing pool's Stream_Id) and exit")
     ap.add_argument("--trace-stream", default=None,
                     help="with --trace: only dispatches of this Stream_Id")
     ap.add_argument("--scales", nargs=2, type=float, default=(1.0, 1.0), metavar=("FETCH", "WRITE"),
@@ -429,6 +490,9 @@ def main():
                     help="with --pmc-summary: also write each kernel class's HBM bytes per "
                          "dispatch (fetch + write, dispatch-weighted over its grids) to OUT")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.trace_stream))
+        return
     if args.pmc_summary:
         table, rows = pmc_summary(args.pmc_summary, args.trace, args.scales[0], args.scales[1],
                                   args.trace_stream)
@@ -561,10 +625,14 @@ def main():
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
     if os.path.exists(tfile):  # HBM bytes per dispatch of each class in a --pmc run of this pass
-        for t in json.load(open(tfile)).get("kernels", []):
-            g = str(dom["grid_items"])
-            if t.get("class") == dom["class"] and g in t.get("grid_bytes", {}):
-                traffic = t["grid_bytes"][g]
+        # Residual GEMM rows carry the op (op_tags): O-proj and FFN2 may share
+        # kernel and grid.
+        tag = {"o_proj_ln": " [o_proj]", "ffn2_ln": " [ffn2]"}.get(dom["op"], "")
+        g = str(dom["grid_items"])
+        for name in (dom["class"] + tag, dom["class"]):
+            for t in json.load(open(tfile)).get("kernels", []):
+                if traffic is None and t.get("class") == name and g in t.get("grid_bytes", {}):
+                    traffic = t["grid_bytes"][g]
     out["roofline"] = {
         "bound": "mfma" if gemm else "hbm", "achieved": ach, "peak": peak,
         "unit": "TFLOP/s" if gemm else "GB/s", "frac": round(ach / peak, 4), "traffic": traffic,

@@ -293,10 +293,12 @@ struct Packed {
 
 // out = LN(A . W^T + bias + residual) over 384-wide rows: one kernel where
 // the GEMM tile owns whole rows, else the residual GEMM and a LayerNorm pass
-// over out, timed as two ops.
+// over out, timed as two ops.  With ln_deferred given, that LayerNorm pass is
+// left to the caller (out holds the rows before it) and *ln_deferred says so.
 bbh_status linear_residual_ln(OpTimer* t, hipStream_t s, int op, const f16* A, const f16* W,
                               const f16* bias, const f16* residual, const f16* gamma,
-                              const f16* beta, f16* out, int M, int K, const char* what) {
+                              const f16* beta, f16* out, int M, int K, const char* what,
+                              bool* ln_deferred = nullptr) {
   const int H = BBH_HIDDEN;
   bool fused;
   const int tile = bbh::gemm_residual_ln_tile(M, K, &fused);
@@ -309,6 +311,10 @@ bbh_status linear_residual_ln(OpTimer* t, hipStream_t s, int op, const f16* A, c
   BBH_TRY(timed_op(t, s, {op, tile, 0, M, H, K, 0.f}, [&] {
     return check_launch(bbh::gemm_residual(A, W, bias, residual, out, M, K, s), what);
   }));
+  if (ln_deferred) {
+    *ln_deferred = true;
+    return BBH_OK;
+  }
   return timed_op(t, s, {BBH_OP_LAYERNORM, -1, 0, M, H, 0, 0.f}, [&] {
     return check_launch(bbh::layernorm(out, nullptr, gamma, beta, out, M, H, BBH_LAYER_NORM_EPS, s),
                         "residual layernorm");
@@ -351,7 +357,8 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
 }
 
 bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                        f16* out, int M, hipStream_t s, OpTimer* t = nullptr) {
+                        f16* out, int M, hipStream_t s, OpTimer* t = nullptr,
+                        bool* ln_deferred = nullptr) {
   const int H = BBH_HIDDEN, F = BBH_FFN_DIM;
   // One kernel for the block at large M; it moves rows in 16-byte pieces
   // (the GEMM path falls back to its any-alignment kernel instead).
@@ -366,7 +373,7 @@ bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16*
                         "ffn1 gemm");
   }));
   return linear_residual_ln(t, s, BBH_OP_FFN2_LN, ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
-                            L.ln2_b, out, M, F, "ffn2 gemm+ln");
+                            L.ln2_b, out, M, F, "ffn2 gemm+ln", ln_deferred);
 }
 
 bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
@@ -377,10 +384,14 @@ bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16
 // Embeddings + 6 layers over the segments' rows; the last layer writes
 // `final_out` (which may be ws->attn_out: the FFN2+LN epilogue reads each
 // residual element before the same thread overwrites it).  Segment g's
-// tokens are at ids + tok[g] (types and masks likewise).
+// tokens are at ids + tok[g] (types and masks likewise).  With
+// final_ln_deferred given, a last LayerNorm that would run as a pass of its
+// own is left to the caller (pool_out) and *final_ln_deferred says so.
 bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
                            const int32_t* types, const int64_t* tok, const Segment* segs,
-                           int n_segs, f16* final_out, hipStream_t s, OpTimer* t = nullptr) {
+                           int n_segs, f16* final_out, hipStream_t s, OpTimer* t = nullptr,
+                           bool* final_ln_deferred = nullptr) {
+  if (final_ln_deferred) *final_ln_deferred = false;
   int M = 0;
   for (int g = 0; g < n_segs; ++g) {
     const Segment& sg = segs[g];
@@ -397,7 +408,8 @@ bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t*
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
     BBH_TRY(run_attention_block(ws, m->layers[i], cur, segs, n_segs, ws->attn_out, M, s, t));
-    BBH_TRY(run_ffn_rows(ws, m->layers[i], ws->attn_out, nxt, M, s, t));
+    BBH_TRY(run_ffn_rows(ws, m->layers[i], ws->attn_out, nxt, M, s, t,
+                         i == BBH_NUM_LAYERS - 1 ? final_ln_deferred : nullptr));
     cur = nxt;
   }
   return BBH_OK;
@@ -426,10 +438,26 @@ bbh_status run_encode_packed(bbh_workspace* ws, const bbh_model* m, const int32_
 
 bbh_status run_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
                       const int32_t* types, const int32_t* mask, f16* final_out, int batch,
-                      int seq, hipStream_t s, OpTimer* t = nullptr) {
+                      int seq, hipStream_t s, OpTimer* t = nullptr,
+                      bool* final_ln_deferred = nullptr) {
   const Segment one{mask, batch, seq, 0};
   const int64_t tok0 = 0;
-  return run_encode_segs(ws, m, ids, types, &tok0, &one, 1, final_out, s, t);
+  return run_encode_segs(ws, m, ids, types, &tok0, &one, 1, final_out, s, t, final_ln_deferred);
+}
+
+// Masked mean pool + L2 normalise of a forward's final rows into out.  If the
+// forward left its last LayerNorm to the pool (final_ln_deferred), the pool
+// normalises each counted row itself, bit for bit as that pass would: one
+// launch fewer.  For callers that do not hand out the hidden rows.
+bbh_status pool_out(OpTimer* t, hipStream_t s, const bbh_model* m, bool ln_deferred,
+                    const f16* hidden, const int32_t* mask, f16* out, int batch, int seq) {
+  return timed_op(t, s, {BBH_OP_POOL, -1, 0, batch, seq, 0, 0.f}, [&] {
+    const bbh_model::Layer& L = m->layers[BBH_NUM_LAYERS - 1];
+    return check_launch(ln_deferred ? bbh::ln_pool_normalize(hidden, mask, L.ln2_g, L.ln2_b,
+                                                             BBH_LAYER_NORM_EPS, out, batch, seq, s)
+                                    : bbh::pool_normalize(hidden, mask, out, batch, seq, s),
+                        "pool+normalize");
+  });
 }
 
 }  // namespace
@@ -886,9 +914,10 @@ bbh_status bbh_embed_noalloc(const bbh_model* m, const int32_t* ids, const int32
   ws.pong = ws.ping + R * H;
   ws.sents = nullptr;  // padded forwards only
   const hipStream_t s = S(stream);
-  BBH_TRY(run_encode(&ws, m, ids, types, mask, ws.attn_out, batch, seq, s));
-  return check_launch(bbh::pool_normalize(ws.attn_out, mask, static_cast<f16*>(emb), batch, seq, s),
-                      "pool+normalize");
+  bool ln_deferred = false;  // no caller sees these rows
+  BBH_TRY(run_encode(&ws, m, ids, types, mask, ws.attn_out, batch, seq, s, nullptr, &ln_deferred));
+  return pool_out(nullptr, s, m, ln_deferred, ws.attn_out, mask, static_cast<f16*>(emb), batch,
+                  seq);
 }
 
 struct bbh_graph {
@@ -1151,19 +1180,15 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
       tok.push_back(tok_offsets[i]);
       row += rows_of(r);
     }
+    bool ln_deferred = false;  // a pool's workspaces are its own
     BBH_TRY(run_encode_segs(w, m, ids, types, tok.data(), segs.data(), (int)segs.size(),
-                            w->attn_out, pool->streams[j], pool->timer));
+                            w->attn_out, pool->streams[j], pool->timer, &ln_deferred));
     for (size_t k = 0; k < segs.size(); ++k) {
       const int i = runs[groups[g].runs[k]].first;
       f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
-      BBH_TRY(timed_op(pool->timer, pool->streams[j],
-                       {BBH_OP_POOL, -1, 0, segs[k].batch, segs[k].seq, 0, 0.f}, [&] {
-                         return check_launch(
-                             bbh::pool_normalize(w->attn_out + segs[k].row * BBH_HIDDEN,
-                                                 segs[k].mask, out, segs[k].batch, segs[k].seq,
-                                                 pool->streams[j]),
-                             "pool+normalize");
-                       }));
+      BBH_TRY(pool_out(pool->timer, pool->streams[j], m, ln_deferred,
+                       w->attn_out + segs[k].row * BBH_HIDDEN, segs[k].mask, out, segs[k].batch,
+                       segs[k].seq));
     }
   }
   for (int j = 0; j < used; ++j) {
@@ -1208,13 +1233,12 @@ bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids
     const hipStream_t st = pool->streams[j];
     bbh_workspace* w = pool->ws[j];
     const int32_t* mk = mask + tok_offsets[i];
+    bool ln_deferred = false;  // a pool's workspaces are its own
     BBH_TRY(run_encode(w, m, ids + tok_offsets[i], types + tok_offsets[i], mk, w->attn_out,
-                       batch_sizes[i], seqs[i], st, pool->timer));
+                       batch_sizes[i], seqs[i], st, pool->timer, &ln_deferred));
     f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
-    return timed_op(pool->timer, st, {BBH_OP_POOL, -1, 0, batch_sizes[i], seqs[i], 0, 0.f}, [&] {
-      return check_launch(bbh::pool_normalize(w->attn_out, mk, out, batch_sizes[i], seqs[i], st),
-                          "pool+normalize");
-    });
+    return pool_out(pool->timer, st, m, ln_deferred, w->attn_out, mk, out, batch_sizes[i],
+                    seqs[i]);
   };
   if (used > 1 && !pool->timer) {
     // Each stream's batches are enqueued by a host thread of its own (the

@@ -120,16 +120,27 @@ __device__ __forceinline__ Affine384 load_affine384(const f16* __restrict__ gamm
   return a;
 }
 
+// fp16 of v * gamma[c] + beta[c] for the lane's column pair j (columns
+// 2 lane + 128 j, +1), the expression every 384-wide LayerNorm row output
+// goes through: an fp32 multiply-add, then the conversion.  The empty asm
+// keeps the compiler from fusing the two into one v_fma_mix*_f16 (a single
+// rounding) in some kernels and not in others.
+__device__ __forceinline__ f16x2 affine384_pair(const float (&v)[6], const Affine384& a, int j) {
+  float x0 = v[2 * j] * (float)a.g[j][0] + (float)a.b[j][0];
+  float x1 = v[2 * j + 1] * (float)a.g[j][1] + (float)a.b[j][1];
+  asm volatile("" : "+v"(x0), "+v"(x1));
+  f16x2 o;
+  o[0] = (f16)x0;
+  o[1] = (f16)x1;
+  return o;
+}
+
 // y[c] = v * gamma[c] + beta[c] for the lane's columns.
 __device__ __forceinline__ void store_affine384(f16* __restrict__ y, const float (&v)[6],
                                                 const Affine384& a, int lane) {
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    f16x2 o;
-    o[0] = (f16)(v[2 * j] * (float)a.g[j][0] + (float)a.b[j][0]);
-    o[1] = (f16)(v[2 * j + 1] * (float)a.g[j][1] + (float)a.b[j][1]);
-    *reinterpret_cast<f16x2*>(y + 2 * lane + 128 * j) = o;
-  }
+  for (int j = 0; j < 3; ++j)
+    *reinterpret_cast<f16x2*>(y + 2 * lane + 128 * j) = affine384_pair(v, a, j);
 }
 
 // D(16x16, fp32) += A(16x32, fp16) . B(32x16, fp16) on the CDNA4 matrix core.

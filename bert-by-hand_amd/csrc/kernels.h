@@ -100,6 +100,11 @@ hipError_t mean_pool(const f16* hidden, const int32_t* mask, f16* out, int batch
 hipError_t l2_normalize(f16* x, int n, int batch, hipStream_t s);
 hipError_t pool_normalize(const f16* hidden, const int32_t* mask, f16* out, int batch,
                           int seq, hipStream_t s);
+// LayerNorm (gamma, beta, eps) of each counted row of y, then pool_normalize:
+// equal to layernorm(y) followed by pool_normalize; y is left as it was.
+hipError_t ln_pool_normalize(const f16* y, const int32_t* mask, const f16* gamma,
+                             const f16* beta, float eps, f16* out, int batch, int seq,
+                             hipStream_t s);
 
 // Exact-erf GELU in place over n values.
 hipError_t gelu(f16* x, size_t n, hipStream_t s);

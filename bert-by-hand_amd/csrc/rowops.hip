@@ -145,10 +145,14 @@ __global__ __launch_bounds__(256) void embedding_kernel(
 // hidden row.  Each wavefront first lists its counted positions in LDS (one
 // ballot per 64 of them), then sums their rows four at a time, so the row
 // loads are issued together instead of one mask-dependent load at a time; the
-// sum order is the same as one position after another.
-template <class Valid, class RowOf>
+// sum order is the same as one position after another.  `xform(a)` maps a
+// loaded row (the lane's three column pairs) to the values that are summed.
+struct RowAsIs {
+  __device__ __forceinline__ void operator()(f16x2 (&)[3]) const {}
+};
+template <class Valid, class RowOf, class Xform = RowAsIs>
 __device__ __forceinline__ void pool_normalize_body(int seq, Valid valid, RowOf row,
-                                                    f16* __restrict__ dst) {
+                                                    f16* __restrict__ dst, Xform xform = {}) {
   __shared__ float part[4][kHidden];
   __shared__ int cnt_part[4];
   __shared__ short plist[4][kMaxPos / 4];
@@ -174,12 +178,14 @@ __device__ __forceinline__ void pool_normalize_body(int seq, Valid valid, RowOf 
       for (int j = 0; j < 3; ++j) a[u][j] = *reinterpret_cast<const f16x2*>(hr + 2 * lane + 128 * j);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      xform(a[u]);
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
         acc[2 * j] += (float)a[u][j][0];
         acc[2 * j + 1] += (float)a[u][j][1];
       }
+    }
   };
   int k = 0;
   for (; k + 4 <= n; k += 4) add_rows(std::integral_constant<int, 4>{}, k);
@@ -222,6 +228,40 @@ __global__ __launch_bounds__(256) void pool_normalize_kernel(const f16* __restri
   pool_normalize_body(
       seq, [&](int p) { return mb[p] != 0; }, [&](int p) { return hb + (size_t)p * kHidden; },
       out + (size_t)b * kHidden);
+}
+
+// The last encoder layer's residual LayerNorm and the pool in one pass: the
+// rows are read before their LayerNorm (y = FFN2 output + residual), each
+// counted row is normalised as ln384 does it, rounded to fp16 the same way,
+// and summed; so the embedding equals ln384 followed by pool_normalize, bit
+// for bit, with one launch and one read of the rows fewer.  Only the pooled
+// rows are normalised, and none is written back.
+struct RowLayerNorm {
+  Affine384 aff;
+  float eps;
+  __device__ __forceinline__ void operator()(f16x2 (&a)[3]) const {
+    float v[6];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      v[2 * j] = (float)a[j][0];
+      v[2 * j + 1] = (float)a[j][1];
+    }
+    ln_row384(v, eps);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) a[j] = affine384_pair(v, aff, j);
+  }
+};
+
+__global__ __launch_bounds__(256) void ln_pool_normalize_kernel(
+    const f16* __restrict__ y, const int32_t* __restrict__ mask, const f16* __restrict__ gamma,
+    const f16* __restrict__ beta, float eps, f16* __restrict__ out, int seq) {
+  const int b = blockIdx.x;
+  const f16* yb = y + (size_t)b * seq * kHidden;
+  const int32_t* mb = mask + (size_t)b * seq;
+  const RowLayerNorm ln{load_affine384(gamma, beta, threadIdx.x & 63), eps};
+  pool_normalize_body(
+      seq, [&](int p) { return mb[p] != 0; }, [&](int p) { return yb + (size_t)p * kHidden; },
+      out + (size_t)b * kHidden, ln);
 }
 
 // Packed sentences: position p of sentence s is hidden row sents[s].row + p.
@@ -367,6 +407,14 @@ hipError_t pool_normalize(const f16* hidden, const int32_t* mask, f16* out, int 
                           hipStream_t s) {
   hipLaunchKernelGGL(pool_normalize_kernel, dim3(batch), dim3(256), 0, s, hidden, mask, out,
                      seq);
+  return hipGetLastError();
+}
+
+hipError_t ln_pool_normalize(const f16* y, const int32_t* mask, const f16* gamma,
+                             const f16* beta, float eps, f16* out, int batch, int seq,
+                             hipStream_t s) {
+  hipLaunchKernelGGL(ln_pool_normalize_kernel, dim3(batch), dim3(256), 0, s, y, mask, gamma, beta,
+                     eps, out, seq);
   return hipGetLastError();
 }
 

@@ -262,6 +262,39 @@ def test_embed_packed_equals_padded_varlen_mix(torch_cuda, model):
     assert np.array_equal(got, want)
 
 
+def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
+    # A pool's forwards leave the last residual LayerNorm to the pooling
+    # kernel (one launch fewer); bert_embed keeps the LayerNorm pass, since its
+    # workspace hands out the final hidden rows.  Same embedding bits, with
+    # empty and full sentences, on one and on three streams, and bert_embed's
+    # hidden rows still normalised.
+    from bbh import engine
+
+    torch = torch_cuda
+    rng = np.random.default_rng(11)
+    batches = []
+    for B, S in [(7, 16), (5, 48), (9, 32), (3, 80), (64, 64), (6, 16)]:
+        n = rng.integers(0, S + 1, size=B)
+        n[0], n[-1] = 0, S
+        mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
+        ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)
+        types = (rng.integers(0, 2, size=(B, S)) * mask).astype(np.int32)
+        batches.append((ids, types, mask))
+    packed = engine.PackedBatches(batches)
+    want = np.concatenate([_embed(torch, ws, model, *b) for b in batches])
+    for n_streams in (1, 3):
+        pool = engine.Pool(n_streams, 64, 80)
+        got = _np(engine.embed_each(pool, model, packed))
+        torch.cuda.synchronize()
+        pool.close()
+        assert np.array_equal(got, want), n_streams
+    # bert_embed's workspace: the final hidden rows are LayerNorm outputs
+    ids, types, mask = batches[4]
+    _embed(torch, ws, model, ids, types, mask)
+    h = ws.hidden(64, 64).float().cpu().numpy()
+    assert np.abs(h.mean(axis=1)).max() < 0.05  # gamma 1, beta 0 in the seeded weights
+
+
 def test_embed_packed_edge_cases(torch_cuda, model):
     # Small forwards (both paths take the separate LayerNorm kernel): bit for
     # bit against the padded path, with lengths 0 (zero embedding) and full,

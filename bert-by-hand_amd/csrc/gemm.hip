@@ -315,9 +315,30 @@ __device__ __forceinline__ bool tile_of(int nb, int mb, int& mi, int& ni) {
 
 // Write ROWS rows of the output tile, staged in LDS as ROWS x OUT_LD fp16,
 // to C rows m0.. with 16-byte stores.
+// A thread's residual chunks of the tile (store_rows' mapping), loaded
+// before the K loop so that their latency hides behind it instead of
+// following it: tiles staged in one pass with at most four chunks a thread.
+template <class C>
+struct ResidualAhead {
+  static constexpr int CPR = C::BN / 8;
+  static constexpr int PER = (C::BM * CPR + C::THREADS - 1) / C::THREADS;
+  static constexpr bool kOn = C::NPASS == 1 && PER <= 4;
+  f16x8 r[kOn ? PER : 1];
+  __device__ __forceinline__ void load(const f16* residual, int ldc, int M, int m0, int n0) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int idx = threadIdx.x + q * C::THREADS;
+      const int row = idx / CPR, c = idx % CPR;
+      if (idx < C::BM * CPR && m0 + row < M)
+        r[q] = *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + row) * ldc + n0 + c * 8);
+    }
+  }
+};
+
 template <class C, int ROWS>
 __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ out, int ldc, int M,
-                                           int m0, int n0, const f16* residual) {
+                                           int m0, int n0, const f16* residual,
+                                           const f16x8* ahead = nullptr) {
   constexpr int CPR = C::BN / 8;
   constexpr int PER = (ROWS * CPR + C::THREADS - 1) / C::THREADS;
   // Unrolled so the residual loads of several rows are in flight together
@@ -331,7 +352,8 @@ __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ ou
       f16x8 v = *reinterpret_cast<const f16x8*>(tile + r * C::OUT_LD + c * 8);
       if (residual) {
         const f16x8 rv =
-            *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + r) * ldc + n0 + c * 8);
+            ahead ? ahead[q]
+                  : *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + r) * ldc + n0 + c * 8);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (f16)((float)v[i] + (float)rv[i]);
       }
@@ -349,6 +371,9 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   int mi, ni;
   if (!tile_of(N / C::BN, (M + C::BM - 1) / C::BM, mi, ni)) return;
   const int m0 = mi * C::BM, n0 = ni * C::BN;
+  constexpr bool kAhead = EPI == kResidual && ResidualAhead<C>::kOn;
+  ResidualAhead<C> ahead;
+  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0);
   f32x16 acc[C::FM][C::FN];
   if constexpr (C::PD > 0)
     mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
@@ -514,7 +539,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       }
     }
     lds_barrier();
-    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr);
+    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr,
+                      kAhead ? ahead.r : nullptr);
     if (p + 1 < C::NPASS) lds_barrier();
   }
 }

@@ -371,28 +371,19 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   int mi, ni;
   if (!tile_of(N / C::BN, (M + C::BM - 1) / C::BM, mi, ni)) return;
   const int m0 = mi * C::BM, n0 = ni * C::BN;
-  constexpr bool kAhead = EPI == kResidual && ResidualAhead<C>::kOn;
-  ResidualAhead<C> ahead;
-  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0);
-  f32x16 acc[C::FM][C::FN];
-  if constexpr (C::PD > 0)
-    mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
-  else
-    mainloop<C>(A, W, M, K, m0, n0, smem, acc);
-
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int r32 = lane & 31, kh = lane >> 5;
-  constexpr int PR = C::BM / C::NPASS;  // tile rows staged per pass
-  f16* tile = smem;                     // PR x OUT_LD fp16
-  float* red = reinterpret_cast<float*>(smem + PR * C::OUT_LD);  // [2][WN][BM]
-  float mean[C::FM], rstd[C::FM];
 
   // Per-column operands (bias; gamma and beta for LayerNorm) depend only on
   // the lane's columns.  Tiles with room in registers load them once, all
   // together, so their latency is paid once per tile instead of once per
   // 32x32 block; the 192-accumulator tiles load them once per column block.
+  // Tiles with one or two 32-column blocks per wavefront and no LayerNorm
+  // (8-16 VGPRs) load them before the K loop, as they do the residual, so
+  // the loads' latency hides behind it.
   constexpr bool kHoist = C::FM * C::FN <= 8;
+  constexpr bool kColsAhead = kHoist && EPI != kLayerNorm && C::FN <= 2;
   constexpr int HN = kHoist ? C::FN : 1;
   f16x4 bvs[HN][4], gvs[EPI == kLayerNorm ? HN : 1][4], evs[EPI == kLayerNorm ? HN : 1][4];
   auto load_cols = [&](int fn, int h) {
@@ -406,7 +397,24 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       }
     }
   };
-  if constexpr (kHoist) {
+  if constexpr (kColsAhead) {
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
+  }
+  constexpr bool kAhead = EPI == kResidual && ResidualAhead<C>::kOn;
+  ResidualAhead<C> ahead;
+  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0);
+  f32x16 acc[C::FM][C::FN];
+  if constexpr (C::PD > 0)
+    mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
+  else
+    mainloop<C>(A, W, M, K, m0, n0, smem, acc);
+
+  constexpr int PR = C::BM / C::NPASS;  // tile rows staged per pass
+  f16* tile = smem;                     // PR x OUT_LD fp16
+  float* red = reinterpret_cast<float*>(smem + PR * C::OUT_LD);  // [2][WN][BM]
+  float mean[C::FM], rstd[C::FM];
+  if constexpr (kHoist && !kColsAhead) {
 #pragma unroll
     for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
   }

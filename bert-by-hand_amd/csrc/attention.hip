@@ -251,7 +251,7 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
     float inv[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const float lt = l[t] + __shfl_xor(l[t], 32, kWave);
+      const float lt = xor32_sum(l[t]);
       inv[t] = lt > 0.f ? 1.0f / lt : 0.f;
     }
     if constexpr (!(F & 1)) {

@@ -24,32 +24,71 @@ constexpr int kMaxPos = 512;
 constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr int kTypes = 2;
 
-// Sum / max over the 64 lanes of a wavefront (butterfly, every lane gets it).
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+// Lane exchanges without the LDS.  __shfl_xor compiles to ds_bpermute, an
+// LDS operation with LDS latency (and queued behind the kernel's other LDS
+// traffic); these use the VALU.  xor_*(v, f) returns f(v, v of lane l ^ d):
+//  - d = 32, 16: v_permlane32_swap / v_permlane16_swap, which hand every lane
+//    the low- and the high-half value; f(low, high) equals f(v, partner) bit
+//    for bit for f = + and fmax (both commutative).
+//  - d = 8: DPP row_ror:8 (within a 16-lane row, l -> l ^ 8).
+//  - d = 4: DPP row_shl:4 (reads lane l + 4) or row_shr:4 (lane l - 4), by
+//    bit 2 of the lane.
+//  - d = 2, 1: DPP quad_perm [2,3,0,1] / [1,0,3,2].
+// (Lane mappings checked on the device.)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+template <int D, class F>
+__device__ __forceinline__ float xor_op(float v, F f) {
+  if constexpr (D == 32) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return f(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  } else if constexpr (D == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return f(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  } else if constexpr (D == 8) {
+    return f(v, dpp<0x128>(v));
+  } else if constexpr (D == 4) {
+    const float up = dpp<0x104>(v), down = dpp<0x114>(v);
+    return f(v, (threadIdx.x & 4) ? down : up);
+  } else if constexpr (D == 2) {
+    return f(v, dpp<0x4E>(v));
+  } else {
+    static_assert(D == 1, "xor distance");
+    return f(v, dpp<0xB1>(v));
+  }
+}
+struct AddOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+// Sum / max over the 64 lanes of a wavefront (butterfly at distances 32, 16,
+// ..., 1; every lane gets it).
+template <class F>
+__device__ __forceinline__ float wave_reduce(float v, F f) {
+  v = xor_op<32>(v, f);
+  v = xor_op<16>(v, f);
+  v = xor_op<8>(v, f);
+  v = xor_op<4>(v, f);
+  v = xor_op<2>(v, f);
+  return xor_op<1>(v, f);
 }
+__device__ inline float wave_sum(float v) { return wave_reduce(v, AddOp{}); }
+__device__ inline float wave_max(float v) { return wave_reduce(v, MaxOp{}); }
 
 // Reduction over the four 16-lane groups that share lane % 16 (the lanes that
 // hold one row / column of a 16x16 MFMA tile).
-__device__ inline float group4_sum(float v) {
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
-}
+__device__ inline float group4_sum(float v) { return xor_op<32>(xor_op<16>(v, AddOp{}), AddOp{}); }
+__device__ inline float group4_max(float v) { return xor_op<32>(xor_op<16>(v, MaxOp{}), MaxOp{}); }
 
-__device__ inline float group4_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  v = fmaxf(v, __shfl_xor(v, 32, kWave));
-  return v;
-}
+// v + the value of lane l ^ 32 (equal to v + __shfl_xor(v, 32) bit for bit).
+__device__ inline float xor32_sum(float v) { return xor_op<32>(v, AddOp{}); }
 
 // Exact GELU, x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), with the device
 // library's erff (src/kernels/matmul.cu:27-28 uses the same definition).

@@ -322,7 +322,7 @@ __global__ __launch_bounds__(ffnf::THREADS) void ffn_fused_kernel(
           for (int b = 3 * gg; b < 3 * gg + 3; ++b)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sg[gg] += y[b][i];
-          sg[gg] += __shfl_xor(sg[gg], 32, kWave);
+          sg[gg] = xor32_sum(sg[gg]);
         }
         lds_barrier();
         if (kh == 0) {
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(ffnf::THREADS) void ffn_fused_kernel(
               y[b][i] -= mean;  // kept centred: the output pass reuses the difference
               qg += y[b][i] * y[b][i];
             }
-          qg += __shfl_xor(qg, 32, kWave);
+          qg = xor32_sum(qg);
           if (kh == 0) red[128 + (2 * half + gg) * 32 + r32] = qg;
         }
         lds_barrier();

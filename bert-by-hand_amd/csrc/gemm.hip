@@ -475,7 +475,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       for (int fn = 0; fn < C::FN; ++fn)
 #pragma unroll
         for (int i = 0; i < 16; ++i) s += acc[fm][fn][i];
-      s += __shfl_xor(s, 32, kWave);
+      s = xor32_sum(s);
       if (kh == 0) red[wn * C::BM + wm * C::TM + fm * 32 + r32] = s;
     }
     lds_barrier();
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
           const float d = acc[fm][fn][i] - mean[fm];
           q += d * d;
         }
-      q += __shfl_xor(q, 32, kWave);
+      q = xor32_sum(q);
       if (kh == 0) red[(C::WN + wn) * C::BM + row] = q;
     }
     lds_barrier();
@@ -772,7 +772,7 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
       float sm = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm += acc[e];
-      sm += __shfl_xor(sm, 32, kWave);
+      sm = xor32_sum(sm);
       if (kh == 0) red[wave * 32 + r32] = sm;
       lds_barrier();
       float t = 0.f;
@@ -785,7 +785,7 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
         const float d = acc[e] - mean;
         q += d * d;
       }
-      q += __shfl_xor(q, 32, kWave);
+      q = xor32_sum(q);
       if (kh == 0) red[(NW + wave) * 32 + r32] = q;
       lds_barrier();
       float t2 = 0.f;

@@ -920,6 +920,7 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 // of the sweep that chose them are compiled only with -DBBH_TUNING.
 //   id  tile      wave tile  SA   LDS
 //    0  64x64     32x32      4    48 KB
+//    1  64x128    32x64      4    64 KB
 //   14  64x384    64x96      2   112 KB   (owns whole 384-wide rows)
 //   8 wavefronts (2 per SIMD):
 //   18  128x384   64x96      4   160 KB   (owns whole rows)
@@ -934,6 +935,7 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 // The table itself: X(id, BM, BN, WM, WN, SA, PD, SW).
 #define BBH_TILES(X) \
   X(0, 64, 64, 2, 2, 4, 0, 2) \
+  X(1, 64, 128, 2, 2, 4, 0, 2) \
   X(14, 64, 384, 1, 4, 2, 0, 2) \
   X(18, 128, 384, 2, 4, 4, 0, 2) \
   X(19, 256, 192, 4, 2, 3, 0, 2) \
@@ -944,9 +946,8 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
   X(32, 128, 192, 4, 2, 2, 2, 2)
 
 #ifdef BBH_TUNING
-// The rest of the sweep (ids 1-13, 15-17, 20-25, 27, 29).
+// The rest of the sweep (ids 2-13, 15-17, 20-25, 27, 29).
 #define BBH_TUNING_TILES(X) \
-  X(1, 64, 128, 2, 2, 4, 0, 2) \
   X(2, 128, 64, 2, 2, 4, 0, 2) \
   X(3, 128, 128, 2, 2, 4, 0, 2) \
   X(4, 256, 128, 2, 2, 3, 0, 2) \
@@ -1021,19 +1022,25 @@ const char* tile_name(int id) {
 // (1536, 384) FFN1, (384, 384) O-proj and (384, 1536) FFN2.  QKV and FFN1 at
 // large M run on the weight-resident kernel instead (wres_ok).  Small M wants
 // many small tiles (latency, CU coverage); large M wants big tiles (L2 and
-// LDS traffic per MFMA).  FFN2 from 2049 to 4096 rows takes the copy-ring
-// 64x64 tile (0), not the register-staged one (26): equal alone, 1.8% ahead
-// in the per-batch pass on three streams, where its L2 -> LDS copies do not
-// go through VGPRs (~57 against ~15-18 B/clk per CU).
+// LDS traffic per MFMA).  From 1025 to 4096 rows (the batch-64 forwards of
+// the length buckets) the choice comes from the per-batch pass on three
+// streams, where the kernels of other forwards share the CUs, rather than
+// from one kernel alone: every tile tried for each (shape, M) with the
+// others fixed, then the winners confirmed in interleaved repeats.  FFN1
+// takes the 128x128 register-staged tile (30) from 1025 rows and FFN2 the
+// 64x128 copy-ring tile (1) from 2049 rows: 391K -> 409K sentences/s for
+// the pass.  Fewer, larger tiles move fewer bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
-  if (M <= 2048)
+  if (M <= 1024)
     id = qkv ? 30 : ffn1 ? 0 : 26;
+  else if (M <= 2048)
+    id = qkv ? 30 : ffn1 ? 30 : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? 26 : 0;
+    id = qkv ? 30 : ffn1 ? 30 : wide_k ? 1 : 0;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : 0;
+    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 1 : 0;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

@@ -7,7 +7,7 @@ rows).  One step = one bert_embed per batch at its padded length, as the
 reference's corpus benchmark loops over its batches (bench/corpus.cu:120-132):
 bbh_embed_each runs each batch as its own forward (nothing merged, every
 padding row computed) and spreads the 32 forwards over EACH_STREAMS
-concurrent HIP streams, one workspace each.  value = sentences/s over the K
+concurrent HIP streams (the pool's and the caller's), one workspace each.  value = sentences/s over the K
 timed steps, inputs pre-uploaded to HBM.
 
 The roofline names the dominant kernel class of that pass: the same pass on a
@@ -38,11 +38,12 @@ for _p in (ROOT, os.path.join(ROOT, "bert-by-hand_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-EACH_STREAMS = 3  # concurrent per-batch forwards.  HIP maps streams onto GPU_MAX_HW_QUEUES = 4
-#                  hardware queues and the caller's stream holds one, so 3 pool streams get
-#                  a queue each (measured per pass: 1 stream 10.5 ms, 2 6.6, 3 5.4, 4 6.2-7.0
-#                  (two streams share a queue), 6 5.4-5.8; with 5-8 hardware queues every
-#                  configuration above 3 busy queues took 11-22 ms)
+EACH_STREAMS = 4  # concurrent per-batch forwards (pool slots): 3 pool streams and the caller's
+#                  stream.  HIP maps streams onto GPU_MAX_HW_QUEUES = 4 hardware queues and
+#                  the caller's stream holds one, so 4 slots keep every queue busy (per pass:
+#                  3 pool streams beside an idle caller 5.07 ms, 4 slots 4.33 ms; earlier,
+#                  4 pool streams beside the caller, two sharing a queue, 6.2-7.0 ms; with
+#                  5-8 hardware queues every configuration above 3 busy queues took 11-22 ms)
 POOL_BATCH = 1024  # workspace rows of the packed / merged pool = POOL_BATCH * 64
 PEAK_FP16_DENSE = 2.5e15  # MI355X published dense fp16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12  # B/s
@@ -557,7 +558,8 @@ def main():
     # The 32 consecutive batches of 64, each at its own padded round16 length,
     # pre-uploaded back to back; one step = bert_embed on every batch
     # (bbh_embed_each: one forward per batch, nothing merged, every padding
-    # row computed), the batches spread over EACH_STREAMS pool streams.
+    # row computed), the batches spread over EACH_STREAMS pool slots (the last
+    # one on the caller's stream).
     batches = synth.varlen_mix()
     n_sent = sum(b[0].shape[0] for b in batches)
     padded_rows = int(sum(b[0].size for b in batches))
@@ -591,7 +593,8 @@ def main():
                                f"{real_tokens} valid tokens); one step = one bert_embed per "
                                "batch at its padded length (bbh_embed_each: nothing merged, "
                                "every padding row computed), the 32 forwards spread over "
-                               f"{EACH_STREAMS} concurrent HIP streams with one workspace each",
+                               f"{EACH_STREAMS} concurrent HIP streams ({EACH_STREAMS - 1} pool "
+                               "streams and the caller's) with one workspace each",
                    "streams": EACH_STREAMS,
                    "model": "MiniLM-L6 (6 layers, hidden 384, 12x32 heads, FFN 1536)",
                    "global_batch": 64,

@@ -206,9 +206,12 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
  * forward at its own (batch_sizes[i], seqs[i]) shape: nothing is merged and
  * every padding row is computed, so each batch's embeddings are bit for bit
  * those of bbh_embed on that batch.  Batch i goes, in batch order, to the
- * stream with the fewest rows so far; the call orders itself after prior
- * work on `stream`, makes later work on `stream` wait for all batches, and
- * returns without a host sync.  With more than one stream in use (and op
+ * slot with the fewest rows so far.  A pool of n >= 2 slots runs slots
+ * 0 .. n-2 on its own streams and slot n-1 on `stream` itself, so n = 4 keeps
+ * HIP's 4 hardware queues per process (GPU_MAX_HW_QUEUES) busy; one slot
+ * runs on the pool's stream.  The call orders itself after prior work on
+ * `stream`, makes later work on `stream` wait for all batches, and returns
+ * without a host sync.  With more than one stream in use (and op
  * timing off) each stream's launches are enqueued by a host thread of its
  * own, started and joined inside the call; the caller's current HIP device
  * is made current in those threads. */

@@ -266,8 +266,11 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
     # A pool's forwards leave the last residual LayerNorm to the pooling
     # kernel (one launch fewer); bert_embed keeps the LayerNorm pass, since its
     # workspace hands out the final hidden rows.  Same embedding bits, with
-    # empty and full sentences, on one and on three streams, and bert_embed's
-    # hidden rows still normalised.
+    # empty and full sentences, on 1, 2, 4 and 8 slots (from 2 slots the last
+    # one runs on the caller's stream; with 8 it gets no batch), with the
+    # default and with a stream of the caller's own, and bert_embed's hidden
+    # rows still normalised.  Op timing with a slot on the caller's stream:
+    # one record per launch, each finished when read.
     from bbh import engine
 
     torch = torch_cuda
@@ -282,12 +285,23 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
         batches.append((ids, types, mask))
     packed = engine.PackedBatches(batches)
     want = np.concatenate([_embed(torch, ws, model, *b) for b in batches])
-    for n_streams in (1, 3):
+    for n_streams in (1, 2, 4, 8):
         pool = engine.Pool(n_streams, 64, 80)
         got = _np(engine.embed_each(pool, model, packed))
         torch.cuda.synchronize()
-        pool.close()
         assert np.array_equal(got, want), n_streams
+        side = torch.cuda.Stream()  # default priority
+        with torch.cuda.stream(side):
+            emb = engine.embed_each(pool, model, packed, stream=side.cuda_stream)
+        side.synchronize()
+        assert np.array_equal(_np(emb), want), (n_streams, "own stream")
+        if n_streams == 4:
+            pool.timing(4096)
+            engine.embed_each(pool, model, packed)
+            recs = pool.timing_read()
+            pool.timing(0)
+            assert len(recs) > 6 * 40 and all(r["ms"] > 0 for r in recs)
+        pool.close()
     # bert_embed's workspace: the final hidden rows are LayerNorm outputs
     ids, types, mask = batches[4]
     _embed(torch, ws, model, ids, types, mask)

@@ -1023,13 +1023,14 @@ const char* tile_name(int id) {
 // large M run on the weight-resident kernel instead (wres_ok).  Small M wants
 // many small tiles (latency, CU coverage); large M wants big tiles (L2 and
 // LDS traffic per MFMA).  From 1025 to 4096 rows (the batch-64 forwards of
-// the length buckets) the choice comes from the per-batch pass on three
-// streams, where the kernels of other forwards share the CUs, rather than
-// from one kernel alone: every tile tried for each (shape, M) with the
-// others fixed, then the winners confirmed in interleaved repeats.  FFN1
-// takes the 128x128 register-staged tile (30) from 1025 rows and FFN2 the
-// 64x128 copy-ring tile (1) from 2049 rows: 391K -> 409K sentences/s for
-// the pass.  Fewer, larger tiles move fewer bytes L2 -> CU per FLOP.
+// the length buckets) the choice comes from the concurrent per-batch pass,
+// where the kernels of other forwards share the CUs, rather than from one
+// kernel alone: every tile tried for each (shape, M) with the others fixed,
+// then the winners confirmed in interleaved repeats.  FFN1 takes the 128x128
+// register-staged tile (30) from 1025 rows and FFN2 the 64x128 copy-ring
+// tile (1) from 2049 rows: 391K -> 409K sentences/s for the pass on three
+// streams; a sweep on four found no tile ahead of these.  Fewer, larger
+// tiles move fewer bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;

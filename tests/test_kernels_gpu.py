@@ -28,6 +28,8 @@ GEMM_SHAPES = [
     (16, 1152, 384, False), (48, 384, 384, False), (1040, 1536, 384, True),
     (1024, 384, 1536, False), (3072, 1152, 384, False), (8192, 1536, 384, True),
     (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
+    # the batch-64 buckets' tiles, ragged: 128x128 for FFN1, 64x128 for FFN2
+    (2500, 1536, 384, True), (3000, 384, 1536, False),
     # large-M tiles (cfg5 runs M = 131072 end to end), one shape per tile bucket
     (12288, 1152, 384, False), (16384, 384, 1536, False),
     (32768, 1152, 384, False), (32768, 1536, 384, True), (32768, 384, 384, False),
@@ -129,6 +131,7 @@ def test_linear_reference_kat(torch_cuda, kats, tag):
 
 
 @pytest.mark.parametrize("M,K", [(16, 384), (33, 384), (1024, 1536), (8192, 1536), (3000, 384),
+                                 (2100, 1536), (3000, 1536),  # the 64x128 tile, ragged
                                  (12288, 384), (16384, 1536), (32768, 384), (32768, 1536),
                                  (70001, 384)])  # the weight-resident kernel, ragged last tile
 def test_linear_residual_layernorm(torch_cuda, M, K):

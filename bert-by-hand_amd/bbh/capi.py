@@ -69,6 +69,8 @@ SIGNATURES = {
                                c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "bbh_embed_packed": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "bbh_pool_busy": (c_int, [c_void_p, ctypes.POINTER(c_int)]),
+    "bbh_pool_fail_at": (c_int, [c_void_p, c_int]),
     "bbh_pool_timing": (c_int, [c_void_p, c_int]),
     "bbh_pool_timing_read": (c_int, [c_void_p, ctypes.POINTER(LaunchTime), c_int,
                                      ctypes.POINTER(c_int)]),

@@ -182,6 +182,16 @@ class Pool:
         return [dict(op=self.OPS[r.op], tile=r.tile, fused_ln=int(r.fused_ln), m=r.m, n=r.n,
                      k=r.k, ms=r.ms) for r in buf[:cnt.value]]
 
+    def busy(self) -> int:
+        """Pool streams (and caller-stream workspaces) with work pending."""
+        n = ctypes.c_int()
+        call("bbh_pool_busy", self.handle, ctypes.byref(n))
+        return n.value
+
+    def fail_at(self, batch: int):
+        """Test hook: later calls fail on reaching batch / group / forward `batch`."""
+        call("bbh_pool_fail_at", self.handle, batch)
+
     def close(self):
         if self.handle:
             call("bbh_pool_free", self.handle)

@@ -22,6 +22,8 @@
 #include <string>
 #include <algorithm>
 #include <map>
+#include <condition_variable>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -989,7 +991,14 @@ struct bbh_pool {
   std::vector<hipEvent_t> done;  // one per stream, recorded at the end of a call
   hipEvent_t fork = nullptr;
   std::vector<bbh_workspace*> ws;
+  // ws_free[j]: recorded by whichever stream last used workspace j, and
+  // waited on by the next one.  bbh_embed_each runs slot n-1 on the caller's
+  // stream while the other entry points run workspace n-1 on the pool's own
+  // stream n-1, so calls from different streams stay ordered on it.
+  std::vector<hipEvent_t> ws_free;
+  int device = 0;  // the device the pool was created on
   OpTimer* timer = nullptr;  // bbh_pool_timing
+  int fail_at = -1;          // bbh_pool_fail_at (test hook)
   // bbh_embed_packed: plans go host -> device from pinned memory, two slots
   // used alternately by consecutive calls; a slot is rewritten only after the
   // copies that last read it (events per stream) have completed.
@@ -1000,16 +1009,128 @@ struct bbh_pool {
     std::vector<bool> pending;
   } slot[2];
   int next_slot = 0;
+  // Enqueue threads for slots 1 .. n-1 of bbh_embed_each, created with the
+  // pool: each waits for a new generation, runs the job for its slot if the
+  // call uses it, and reports back.
+  struct Workers {
+    std::vector<std::thread> th;
+    std::mutex mu;
+    std::condition_variable go, done;
+    uint64_t gen = 0;
+    int active = 0, remaining = 0;
+    bool stop = false;
+    std::function<void(int)> job;
+  } wk;
 };
 
+namespace {
+
+void worker_loop(bbh_pool* p, int j) {
+  bbh_pool::Workers& w = p->wk;
+  const bool dev_ok = hipSetDevice(p->device) == hipSuccess;
+  uint64_t seen = 0;
+  std::unique_lock<std::mutex> lk(w.mu);
+  for (;;) {
+    w.go.wait(lk, [&] { return w.stop || w.gen != seen; });
+    if (w.stop) return;
+    seen = w.gen;
+    const bool mine = j < w.active;
+    std::function<void(int)> f = w.job;
+    lk.unlock();
+    if (mine) {
+      if (dev_ok)
+        f(j);
+      else
+        f(-1 - j);  // reports that the thread could not make the device current
+    }
+    lk.lock();
+    if (mine && --w.remaining == 0) w.done.notify_all();
+  }
+}
+
+// Runs job(0) on the calling thread and job(j), 1 <= j < active, on the
+// pool's threads; returns when all have finished.
+void run_on_workers(bbh_pool* p, int active, const std::function<void(int)>& job) {
+  bbh_pool::Workers& w = p->wk;
+  {
+    std::lock_guard<std::mutex> lk(w.mu);
+    w.job = job;
+    w.active = active;
+    w.remaining = active - 1;
+    ++w.gen;
+  }
+  w.go.notify_all();
+  job(0);
+  std::unique_lock<std::mutex> lk(w.mu);
+  w.done.wait(lk, [&] { return w.remaining == 0; });
+  w.job = nullptr;
+}
+
+// The fork/join of a pool call.  use(j, s) orders stream s after the last
+// use of workspace j (and after the caller's prior work, for a pool stream);
+// the destructor, on every exit of the call, records each used workspace's
+// ws_free event on the stream that used it and makes the caller's stream
+// wait for every pool stream the call forked: later work on the caller's
+// stream (freeing emb, say) is ordered after everything the call enqueued,
+// also when it fails part-way.  finish() does the same and reports errors.
+class PoolCall {
+ public:
+  PoolCall(bbh_pool* p, hipStream_t caller) : p_(p), caller_(caller), stream_of_(p->ws.size()) {}
+  ~PoolCall() { (void)finish(); }
+  bbh_status begin() {
+    BBH_HIP(hipEventRecord(p_->fork, caller_), "hipEventRecord(fork)");
+    return BBH_OK;
+  }
+  bbh_status use(int j, hipStream_t s) {
+    if (stream_of_[j]) return BBH_OK;
+    if (s != caller_) BBH_HIP(hipStreamWaitEvent(s, p_->fork, 0), "hipStreamWaitEvent(fork)");
+    BBH_HIP(hipStreamWaitEvent(s, p_->ws_free[j], 0), "hipStreamWaitEvent(workspace)");
+    stream_of_[j] = s;
+    return BBH_OK;
+  }
+  bbh_status finish() {
+    bbh_status first = BBH_OK;
+    auto keep = [&](hipError_t e, const char* what) {
+      if (e != hipSuccess && first == BBH_OK) first = hip_fail(e, what);
+    };
+    for (size_t j = 0; j < stream_of_.size(); ++j) {
+      const hipStream_t s = stream_of_[j];
+      if (!s) continue;
+      keep(hipEventRecord(p_->ws_free[j], s), "hipEventRecord(workspace)");
+      if (s != caller_) {
+        keep(hipEventRecord(p_->done[j], s), "hipEventRecord(join)");
+        keep(hipStreamWaitEvent(caller_, p_->done[j], 0), "hipStreamWaitEvent(join)");
+      }
+      stream_of_[j] = nullptr;
+    }
+    return first;
+  }
+
+ private:
+  bbh_pool* p_;
+  hipStream_t caller_;
+  std::vector<hipStream_t> stream_of_;  // per workspace: the stream that used it, or null
+};
+
+}  // namespace
+
 static void pool_release(bbh_pool* p) {
+  {
+    std::lock_guard<std::mutex> lk(p->wk.mu);
+    p->wk.stop = true;
+  }
+  p->wk.go.notify_all();
+  for (auto& t : p->wk.th) t.join();
   for (auto st : p->streams) (void)hipStreamSynchronize(st);
+  // the caller's stream may have used the last workspace
+  for (auto e : p->ws_free) (void)hipEventSynchronize(e);
   for (auto& sl : p->slot) {
     for (auto e : sl.copied) (void)hipEventDestroy(e);
     if (sl.host) (void)hipHostFree(sl.host);
   }
   delete p->timer;
   for (auto w : p->ws) bbh_workspace_free(w);
+  for (auto e : p->ws_free) (void)hipEventDestroy(e);
   for (auto e : p->done) (void)hipEventDestroy(e);
   for (auto s : p->streams) (void)hipStreamDestroy(s);
   if (p->fork) (void)hipEventDestroy(p->fork);
@@ -1020,7 +1141,8 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
   if (!out) return fail(BBH_ERR_INVALID_ARG, "null out");
   if (n_streams < 1 || n_streams > 64) return fail(BBH_ERR_INVALID_ARG, "n_streams must be in [1, 64]");
   bbh_pool* p = new bbh_pool();
-  hipError_t e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
+  hipError_t e = hipGetDevice(&p->device);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
   if (e != hipSuccess) {
     pool_release(p);
     return hip_fail(e, "hipEventCreate");
@@ -1033,13 +1155,15 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
       return hip_fail(e, "hipStreamCreate");
     }
     p->streams.push_back(st);
-    hipEvent_t ev;
-    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
-    if (e != hipSuccess) {
-      pool_release(p);
-      return hip_fail(e, "hipEventCreate");
+    for (auto* evs : {&p->done, &p->ws_free}) {
+      hipEvent_t ev;
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e != hipSuccess) {
+        pool_release(p);
+        return hip_fail(e, "hipEventCreate");
+      }
+      evs->push_back(ev);
     }
-    p->done.push_back(ev);
     bbh_workspace* w = nullptr;
     bbh_status st2 = bbh_workspace_create(max_batch, max_seq, &w);
     if (st2 != BBH_OK) {
@@ -1059,7 +1183,40 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
       sl.pending.push_back(false);
     }
   }
+  try {
+    for (int j = 1; j < n_streams; ++j) p->wk.th.emplace_back(worker_loop, p, j);
+  } catch (const std::exception& ex) {
+    pool_release(p);
+    return fail(BBH_ERR_INVALID_ARG, std::string("pool threads: ") + ex.what());
+  }
   *out = p;
+  return BBH_OK;
+}
+
+bbh_status bbh_pool_fail_at(bbh_pool* pool, int batch) {
+  if (!pool) return fail(BBH_ERR_INVALID_ARG, "null pool");
+  pool->fail_at = batch < 0 ? -1 : batch;
+  return BBH_OK;
+}
+
+bbh_status bbh_pool_busy(bbh_pool* pool, int* busy) {
+  if (!pool || !busy) return fail(BBH_ERR_INVALID_ARG, "null argument");
+  int n = 0;
+  for (auto st : pool->streams) {
+    const hipError_t e = hipStreamQuery(st);
+    if (e == hipErrorNotReady)
+      ++n;
+    else if (e != hipSuccess)
+      return hip_fail(e, "hipStreamQuery");
+  }
+  for (auto ev : pool->ws_free) {  // work a call ran on the caller's stream
+    const hipError_t e = hipEventQuery(ev);
+    if (e == hipErrorNotReady)
+      ++n;
+    else if (e != hipSuccess)
+      return hip_fail(e, "hipEventQuery");
+  }
+  *busy = n;
   return BBH_OK;
 }
 
@@ -1161,15 +1318,16 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     stream_of[g] = j;
     load[j] += groups[g].rows;
   }
-  const hipStream_t caller = S(stream);
-  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
-  const int used = n_groups < n ? n_groups : n;  // streams with work: the first `used`
-  for (int j = 0; j < used; ++j)
-    BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
+  PoolCall call(pool, S(stream));
+  BBH_TRY(call.begin());
   std::vector<Segment> segs;
   std::vector<int64_t> tok;
-  for (int g : order) {
+  for (int q = 0; q < n_groups; ++q) {
+    const int g = order[q];
+    if (q == pool->fail_at)
+      return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: group " + std::to_string(q));
     const int j = stream_of[g];
+    BBH_TRY(call.use(j, pool->streams[j]));
     bbh_workspace* w = pool->ws[j];
     segs.clear();
     tok.clear();
@@ -1191,11 +1349,7 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
                        segs[k].seq));
     }
   }
-  for (int j = 0; j < used; ++j) {
-    BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
-    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
-  }
-  return BBH_OK;
+  return call.finish();
 }
 
 bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids,
@@ -1231,12 +1385,13 @@ bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids
   // against 3 pool streams beside an idle caller; 2 pool streams + the
   // caller's run like 3 pool streams).
   auto slot_stream = [&](int j) { return n > 1 && j == n - 1 ? caller : pool->streams[j]; };
-  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
+  PoolCall call(pool, caller);
+  BBH_TRY(call.begin());
   const int used = n_batches < n ? n_batches : n;  // every batch so far went to an empty stream
-  for (int j = 0; j < used; ++j)
-    if (slot_stream(j) != caller)
-      BBH_HIP(hipStreamWaitEvent(slot_stream(j), pool->fork, 0), "hipStreamWaitEvent(fork)");
+  for (int j = 0; j < used; ++j) BBH_TRY(call.use(j, slot_stream(j)));
   auto one = [&](int i) -> bbh_status {
+    if (i == pool->fail_at)
+      return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: batch " + std::to_string(i));
     const int j = stream_of[i];
     const hipStream_t st = slot_stream(j);
     bbh_workspace* w = pool->ws[j];
@@ -1249,42 +1404,34 @@ bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids
                     seqs[i]);
   };
   if (used > 1 && !pool->timer) {
-    // Each stream's batches are enqueued by a host thread of its own (the
-    // caller's thread takes stream 0).  Enqueueing the ~44 launches of every
-    // batch from one thread cost the host about as long as the GPU took to
-    // run them (4.3-5.1 ms against 5.5 ms for the varlen mix on 3 streams);
-    // launches on different streams do not serialise (1.9-2.0 ms).  With op
-    // timing on, one thread enqueues everything, so the timer's records
-    // stay in launch order.
-    int dev = 0;
-    BBH_HIP(hipGetDevice(&dev), "hipGetDevice");
+    // Each stream's batches are enqueued by a host thread of its own: the
+    // caller's thread takes stream 0, the pool's threads (created with the
+    // pool) the others.  Enqueueing the ~44 launches of every batch from one
+    // thread cost the host about as long as the GPU took to run them
+    // (4.3-5.1 ms against 5.5 ms for the varlen mix on 3 streams); launches
+    // on different streams do not serialise (1.9-2.0 ms).  With op timing
+    // on, one thread enqueues everything, so the timer's records stay in
+    // launch order.  A failing stream stops its own batches; the others run
+    // theirs, and the join (on every exit) orders the caller's stream after
+    // all of them.
     std::vector<bbh_status> res(used, BBH_OK);
     std::vector<std::string> err(used);
-    auto worker = [&](int j) {
-      if (hipSetDevice(dev) != hipSuccess) {
-        res[j] = BBH_ERR_HIP;
-        err[j] = "hipSetDevice in a pool thread";
+    run_on_workers(pool, used, [&](int j) {
+      if (j < 0) {
+        res[-1 - j] = BBH_ERR_HIP;
+        err[-1 - j] = "hipSetDevice in a pool thread";
         return;
       }
       for (int i = 0; i < n_batches && res[j] == BBH_OK; ++i)
         if (stream_of[i] == j) res[j] = one(i);
       if (res[j] != BBH_OK) err[j] = g_err;
-    };
-    std::vector<std::thread> th;
-    for (int j = 1; j < used; ++j) th.emplace_back(worker, j);
-    worker(0);
-    for (auto& t : th) t.join();
+    });
     for (int j = 0; j < used; ++j)
       if (res[j] != BBH_OK) return fail(res[j], err[j]);
   } else {
     for (int i = 0; i < n_batches; ++i) BBH_TRY(one(i));
   }
-  for (int j = 0; j < used; ++j) {
-    if (slot_stream(j) == caller) continue;
-    BBH_HIP(hipEventRecord(pool->done[j], slot_stream(j)), "hipEventRecord(join)");
-    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
-  }
-  return BBH_OK;
+  return call.finish();
 }
 
 bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* ids,
@@ -1367,14 +1514,14 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
     }
   }
   std::copy(all.begin(), all.end(), sl.host);
-  const hipStream_t caller = S(stream);
-  BBH_HIP(hipEventRecord(pool->fork, caller), "hipEventRecord(fork)");
-  const int used = n_fwd < n ? n_fwd : n;
-  for (int j = 0; j < used; ++j)
-    BBH_HIP(hipStreamWaitEvent(pool->streams[j], pool->fork, 0), "hipStreamWaitEvent(fork)");
+  PoolCall call(pool, S(stream));
+  BBH_TRY(call.begin());
   for (int f = 0; f < n_fwd; ++f) {
+    if (f == pool->fail_at)
+      return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: forward " + std::to_string(f));
     const int j = f % n;
     const hipStream_t st = pool->streams[j];
+    BBH_TRY(call.use(j, st));
     bbh_workspace* w = pool->ws[j];
     const size_t first = cut[f], cnt = cut[f + 1] - cut[f];
     int M = 0, max_len = 0;
@@ -1395,11 +1542,7 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
                           "pool+normalize (packed)");
     }));
   }
-  for (int j = 0; j < used; ++j) {
-    BBH_HIP(hipEventRecord(pool->done[j], pool->streams[j]), "hipEventRecord(join)");
-    BBH_HIP(hipStreamWaitEvent(caller, pool->done[j], 0), "hipStreamWaitEvent(join)");
-  }
-  return BBH_OK;
+  return call.finish();
 }
 
 bbh_status bbh_pool_timing(bbh_pool* pool, int capacity) {

@@ -190,10 +190,29 @@ bbh_status bbh_graph_free(bbh_graph *g);
  * fewest rows that has room; they go largest first to the least-loaded
  * stream.  The call orders itself after prior work on `stream` and makes
  * later work on `stream` wait for all batches; it returns without a host
- * sync.  A pool must not be used by two overlapping calls. */
+ * sync.  On every return, errors included, everything the call enqueued is
+ * ordered before later work on `stream`, so a caller may free emb or the
+ * inputs on `stream` after a failed call.  Each pool workspace is also
+ * ordered after its previous use, whichever stream made it, so calls on one
+ * pool from different streams need no host sync between them; calls must
+ * still not overlap in time on the host (a pool is not thread-safe).
+ * bbh_pool_free waits for all of the pool's work, on any stream.  The pool
+ * belongs to the device current at bbh_pool_create; with n_streams >= 2 it
+ * also starts n_streams - 1 host threads (bbh_embed_each), stopped by
+ * bbh_pool_free. */
 typedef struct bbh_pool bbh_pool;
 bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
 bbh_status bbh_pool_free(bbh_pool *pool);
+/* Number of pool streams, plus workspaces last used on a caller's stream,
+ * with work still pending (0 when the pool is idle).  No counterpart in the
+ * reference: for callers that poll instead of synchronising. */
+bbh_status bbh_pool_busy(bbh_pool *pool, int *busy);
+/* Test hook, no counterpart in the reference: later calls on this pool fail
+ * with BBH_ERR_INVALID_ARG when they reach batch (bbh_embed_each), group
+ * (bbh_embed_batches) or forward (bbh_embed_packed) number `batch`, after
+ * enqueueing the earlier ones; a negative value switches it off.  For
+ * exercising the error paths. */
+bbh_status bbh_pool_fail_at(bbh_pool *pool, int batch);
 bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
                              const int32_t *types, const int32_t *mask,
                              const int64_t *tok_offsets, const int *batch_sizes,
@@ -213,8 +232,8 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
  * `stream`, makes later work on `stream` wait for all batches, and returns
  * without a host sync.  With more than one stream in use (and op
  * timing off) each stream's launches are enqueued by a host thread of its
- * own, started and joined inside the call; the caller's current HIP device
- * is made current in those threads. */
+ * own: the caller's thread for slot 0, the pool's threads (created with the
+ * pool, on the pool's device) for the others. */
 bbh_status bbh_embed_each(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
                           const int32_t *types, const int32_t *mask,
                           const int64_t *tok_offsets, const int *batch_sizes, const int *seqs,

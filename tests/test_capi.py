@@ -32,7 +32,7 @@ def test_header_declarations_all_exported():
     from bbh import capi
 
     names = declared_symbols()
-    assert len(names) == 53
+    assert len(names) == 55
     for n in names:
         assert hasattr(L, n), n
     # the Python binding types every declared entry point

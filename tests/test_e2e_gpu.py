@@ -309,6 +309,67 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
     assert np.abs(h.mean(axis=1)).max() < 0.05  # gamma 1, beta 0 in the seeded weights
 
 
+@pytest.mark.parametrize("entry", ["each", "batches", "packed"])
+def test_pool_error_path_joins_caller_stream(torch_cuda, ws, model, entry):
+    # A pool call that fails part-way (the test hook fails batch / group /
+    # forward 3 of bbh_embed_each / _batches / _packed, after the earlier ones
+    # are enqueued on the pool's streams) still orders the caller's stream
+    # after everything it enqueued: once that stream alone is synchronised, no
+    # pool stream has work left.  Every kernel it enqueued runs to the end.
+    # With the hook off, the same pool then gives the sequential results.
+    from bbh import capi, engine, synth
+
+    torch = torch_cuda
+    batches = synth.varlen_mix()[:12]
+    packed = engine.PackedBatches([b[:3] for b in batches])
+    run = {"each": engine.embed_each, "batches": engine.embed_batches,
+           "packed": engine.embed_packed}[entry]
+    pool = engine.Pool(4, 64, 64)
+    side = torch.cuda.Stream()  # default priority
+    pool.fail_at(3)
+    with torch.cuda.stream(side):
+        emb = torch.empty((packed.rows, 384), dtype=torch.float16, device="cuda")
+        with pytest.raises(capi.BBHError, match="bbh_pool_fail_at"):
+            run(pool, model, packed, emb=emb, stream=side.cuda_stream)
+    side.synchronize()
+    assert pool.busy() == 0
+    pool.fail_at(-1)
+    with torch.cuda.stream(side):
+        got = run(pool, model, packed, stream=side.cuda_stream)
+    side.synchronize()
+    assert pool.busy() == 0
+    want = np.concatenate([_embed(torch, ws, model, *b[:3]) for b in batches])
+    assert np.array_equal(_np(got), want)
+    pool.close()
+
+
+def test_pool_calls_from_two_streams_stay_ordered(torch_cuda, ws, model):
+    # bbh_embed_each runs its last slot's workspace on the caller's stream,
+    # bbh_embed_batches and _packed run the same workspace on the pool's own
+    # stream: back-to-back calls on one pool from two caller streams, with no
+    # host sync between them, each give their own batches' embeddings.
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    mix = synth.varlen_mix()
+    a, b = [x[:3] for x in mix[:9]], [x[:3] for x in mix[9:17]]
+    pa, pb = engine.PackedBatches(a), engine.PackedBatches(b)
+    want_a = np.concatenate([_embed(torch, ws, model, *x) for x in a])
+    want_b = np.concatenate([_embed(torch, ws, model, *x) for x in b])
+    pool = engine.Pool(4, 64, 64)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    out = []
+    for s, fn, pk in [(s1, engine.embed_each, pa), (s2, engine.embed_each, pb),
+                      (s2, engine.embed_batches, pa), (s1, engine.embed_each, pb),
+                      (s2, engine.embed_packed, pa), (s1, engine.embed_each, pa)]:
+        with torch.cuda.stream(s):
+            out.append(fn(pool, model, pk, stream=s.cuda_stream))
+    torch.cuda.synchronize()
+    for i, (got, want) in enumerate(zip(out, [want_a, want_b, want_a, want_b, want_a, want_a])):
+        assert np.array_equal(_np(got), want), i
+    pool.close()
+
+
 def test_embed_packed_edge_cases(torch_cuda, model):
     # Small forwards (both paths take the separate LayerNorm kernel): bit for
     # bit against the padded path, with lengths 0 (zero embedding) and full,

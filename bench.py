@@ -471,7 +471,7 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only time a device-to-device copy of BYTES (the calibration kernel "
                          "for the HBM byte counters, and the practical copy bandwidth)")
-    ap.add_argument("--only", choices=["varlen", "cfg5"], default=None,
+    ap.add_argument("--only", choices=["varlen", "cfg2", "cfg3", "cfg5"], default=None,
                     help="only this workload, without the event-timed roofline pass (for "
                          "rocprofv3 counter runs); prints its dict")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV", default=None,
@@ -547,6 +547,19 @@ def main():
                           "ms_per_pass": round(ms, 4), "sentences_per_s": round(2000 / (ms / 1e3), 1)}),
               flush=True)
         return
+    if args.only in ("cfg2", "cfg3"):  # configs[1] / configs[2]: bert_embed, batch 64
+        seq = 16 if args.only == "cfg2" else 128
+        ws = engine.Workspace(64, seq)
+        ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(64, seq))
+        emb = torch.empty((64, 384), dtype=torch.float16, device="cuda")
+        ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask, emb=emb),
+                   args.steps, warmup=args.warmup)
+        print(json.dumps({"workload": f"{args.only}: bert_embed batch 64 x seq {seq}",
+                          "ms_per_forward": round(ms, 4),
+                          "sentences_per_s": round(64 / (ms / 1e3), 1)}), flush=True)
+        ws.close()
+        model.close()
+        return
     if args.only == "cfg5":
         ws = engine.Workspace(256, 512)
         print(json.dumps(run_cfg5(torch, engine, synth, model, ws)), flush=True)
@@ -610,8 +623,8 @@ def main():
     }
 
     # ---- dominant kernel of the default workload ---------------------------
-    # The same per-batch pass on a one-stream pool with per-launch timing: a
-    # pair of HIP events on the pool stream around every op launch, so each
+    # The same per-batch pass on a one-slot pool with per-launch timing: a
+    # pair of HIP events on the caller's stream around every op launch, so each
     # pair brackets that kernel alone with no other stream sharing the GPU.
     n_ops = 32 * (2 + 6 * 7)
     pool1.timing(n_ops)
@@ -647,7 +660,7 @@ def main():
         "algorithmic_flops_per_launch": dom["algorithmic_flops_per_launch"],
         "algorithmic_bytes_per_launch": dom["algorithmic_bytes_per_launch"],
         "share_of_op_time": dom["share_of_op_time"],
-        "timing": f"one-stream pool, event pair per launch, {tsteps} passes"}
+        "timing": f"one-slot pool on the caller's stream, event pair per launch, {tsteps} passes"}
     out["kernel_classes"] = classes[:12]
     log("roofline", out["roofline"])
     for c in classes[:12]:

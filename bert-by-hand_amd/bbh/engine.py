@@ -159,7 +159,8 @@ class EmbedGraph:
 
 
 class Pool:
-    """n HIP streams, each with its own workspace; embed_batches overlaps
+    """n slots, each with its own workspace: slot n-1 runs on the caller's
+    stream, the others on n-1 HIP streams of the pool; embed_batches overlaps
     independent batches across them (replaces a sequential batch loop)."""
 
     def __init__(self, n_streams: int, max_batch: int, max_seq: int):
@@ -183,7 +184,7 @@ class Pool:
                      k=r.k, ms=r.ms) for r in buf[:cnt.value]]
 
     def busy(self) -> int:
-        """Pool streams (and caller-stream workspaces) with work pending."""
+        """Pool streams and workspaces (on any stream) with work pending."""
         n = ctypes.c_int()
         call("bbh_pool_busy", self.handle, ctypes.byref(n))
         return n.value

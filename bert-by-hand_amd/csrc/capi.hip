@@ -126,6 +126,7 @@ struct bbh_workspace {
   size_t bytes = 0;
   f16 *qkv, *ctx, *attn_out, *inter, *ping, *pong;
   bbh::PackedSentence* sents;  // plan of a packed forward: up to `rows` sentences
+  bool shared = false;         // a slot of a multi-slot pool: other forwards run beside
 };
 
 namespace {
@@ -300,18 +301,18 @@ struct Packed {
 bbh_status linear_residual_ln(OpTimer* t, hipStream_t s, int op, const f16* A, const f16* W,
                               const f16* bias, const f16* residual, const f16* gamma,
                               const f16* beta, f16* out, int M, int K, const char* what,
-                              bool* ln_deferred = nullptr) {
+                              bool shared, bool* ln_deferred = nullptr) {
   const int H = BBH_HIDDEN;
   bool fused;
-  const int tile = bbh::gemm_residual_ln_tile(M, K, &fused);
+  const int tile = bbh::gemm_residual_ln_tile(M, K, &fused, shared);
   if (fused)
     return timed_op(t, s, {op, tile, 1, M, H, K, 0.f}, [&] {
       return check_launch(bbh::gemm_residual_ln(A, W, bias, residual, gamma, beta, out, M, K,
-                                                BBH_LAYER_NORM_EPS, s),
+                                                BBH_LAYER_NORM_EPS, s, shared),
                           what);
     });
   BBH_TRY(timed_op(t, s, {op, tile, 0, M, H, K, 0.f}, [&] {
-    return check_launch(bbh::gemm_residual(A, W, bias, residual, out, M, K, s), what);
+    return check_launch(bbh::gemm_residual(A, W, bias, residual, out, M, K, s, shared), what);
   }));
   if (ln_deferred) {
     *ln_deferred = true;
@@ -327,9 +328,10 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
                                const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
                                OpTimer* t = nullptr, const Packed* pk = nullptr) {
   const int H = BBH_HIDDEN;
-  BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H), 0, M, 3 * H, H, 0.f}, [&] {
+  BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H, ws->shared), 0, M, 3 * H, H,
+                          0.f}, [&] {
     return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
-                                  bbh::Act::kNone, s),
+                                  bbh::Act::kNone, s, ws->shared),
                         "qkv gemm");
   }));
   if (pk) {
@@ -348,7 +350,7 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
     }));
   }
   return linear_residual_ln(t, s, BBH_OP_O_PROJ_LN, ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g,
-                            L.ln1_b, out, M, H, "o-proj gemm+ln");
+                            L.ln1_b, out, M, H, "o-proj gemm+ln", ws->shared);
 }
 
 bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
@@ -370,12 +372,14 @@ bbh_status run_ffn_rows(bbh_workspace* ws, const bbh_model::Layer& L, const f16*
                                          out, M, BBH_LAYER_NORM_EPS, s),
                           "ffn (one kernel)");
     });
-  BBH_TRY(timed_op(t, s, {BBH_OP_FFN1_GELU, bbh::gemm_tile(M, F, H), 0, M, F, H, 0.f}, [&] {
-    return check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, F, H, bbh::Act::kGelu, s),
+  BBH_TRY(timed_op(t, s, {BBH_OP_FFN1_GELU, bbh::gemm_tile(M, F, H, ws->shared), 0, M, F, H, 0.f},
+                   [&] {
+    return check_launch(bbh::gemm(hidden, L.f1_w, L.f1_b, ws->inter, M, F, H, bbh::Act::kGelu, s,
+                                  ws->shared),
                         "ffn1 gemm");
   }));
   return linear_residual_ln(t, s, BBH_OP_FFN2_LN, ws->inter, L.f2_w, L.f2_b, hidden, L.ln2_g,
-                            L.ln2_b, out, M, F, "ffn2 gemm+ln", ln_deferred);
+                            L.ln2_b, out, M, F, "ffn2 gemm+ln", ws->shared, ln_deferred);
 }
 
 bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
@@ -987,14 +991,16 @@ bbh_status bbh_encode(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
 }
 
 struct bbh_pool {
+  int n_slots = 0;
+  // Slots 0 .. n_slots-2 run on these streams; the last slot runs on the
+  // stream of each call (slot_stream).
   std::vector<hipStream_t> streams;
-  std::vector<hipEvent_t> done;  // one per stream, recorded at the end of a call
+  std::vector<hipEvent_t> done;  // per slot, recorded at the end of a call
   hipEvent_t fork = nullptr;
-  std::vector<bbh_workspace*> ws;
+  std::vector<bbh_workspace*> ws;  // per slot
   // ws_free[j]: recorded by whichever stream last used workspace j, and
-  // waited on by the next one.  bbh_embed_each runs slot n-1 on the caller's
-  // stream while the other entry points run workspace n-1 on the pool's own
-  // stream n-1, so calls from different streams stay ordered on it.
+  // waited on by the next one, so calls made from different streams stay
+  // ordered on the last slot's workspace.
   std::vector<hipEvent_t> ws_free;
   int device = 0;  // the device the pool was created on
   OpTimer* timer = nullptr;  // bbh_pool_timing
@@ -1073,6 +1079,20 @@ void run_on_workers(bbh_pool* p, int active, const std::function<void(int)>& job
 // wait for every pool stream the call forked: later work on the caller's
 // stream (freeing emb, say) is ordered after everything the call enqueued,
 // also when it fails part-way.  finish() does the same and reports errors.
+// Slot j's stream in a pool call made on `caller`: the last slot runs on the
+// caller's stream itself, the others on the pool's streams.  A one-slot pool
+// thus runs on the caller's stream alone: on a stream of its own, joined into
+// the caller's after every call, the same forwards ran ~0.7 us a kernel slower
+// (varlen mix, 32 batches of 64 on one slot: 10.2 against 9.1 ms a pass; the
+// same with event flags that drop the system-scope fence).  With n slots the
+// caller's hardware queue runs a share instead of only waiting: HIP gives a
+// process GPU_MAX_HW_QUEUES hardware queues (4 by default), so 4 slots keep
+// every queue running a forward (varlen mix per batch: 5.07 -> 4.33 ms a
+// pass against 3 pool streams beside an idle caller).
+hipStream_t slot_stream(const bbh_pool* p, int j, hipStream_t caller) {
+  return j == p->n_slots - 1 ? caller : p->streams[j];
+}
+
 class PoolCall {
  public:
   PoolCall(bbh_pool* p, hipStream_t caller) : p_(p), caller_(caller), stream_of_(p->ws.size()) {}
@@ -1147,14 +1167,17 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
     pool_release(p);
     return hip_fail(e, "hipEventCreate");
   }
+  p->n_slots = n_streams;
   for (int i = 0; i < n_streams; ++i) {
-    hipStream_t st;
-    e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);  // default priority
-    if (e != hipSuccess) {
-      pool_release(p);
-      return hip_fail(e, "hipStreamCreate");
+    if (i < n_streams - 1) {  // the last slot runs on each call's own stream
+      hipStream_t st;
+      e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking);  // default priority
+      if (e != hipSuccess) {
+        pool_release(p);
+        return hip_fail(e, "hipStreamCreate");
+      }
+      p->streams.push_back(st);
     }
-    p->streams.push_back(st);
     for (auto* evs : {&p->done, &p->ws_free}) {
       hipEvent_t ev;
       e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
@@ -1171,6 +1194,7 @@ bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool**
       pool_release(p);
       return fail(st2, msg);
     }
+    w->shared = n_streams > 1;
     p->ws.push_back(w);
     for (auto& sl : p->slot) {
       hipEvent_t ce;
@@ -1236,7 +1260,7 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
       !emb_rows || !emb)
     return fail(BBH_ERR_INVALID_ARG, "bbh_embed_batches: null argument");
   if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
-  const int n = (int)pool->streams.size();
+  const int n = pool->n_slots;
   // validate everything before enqueueing anything
   for (int i = 0; i < n_batches; ++i) {
     bbh_status st = check_shape(pool->ws[i % n], batch_sizes[i], seqs[i]);
@@ -1327,7 +1351,8 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     if (q == pool->fail_at)
       return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: group " + std::to_string(q));
     const int j = stream_of[g];
-    BBH_TRY(call.use(j, pool->streams[j]));
+    const hipStream_t st = slot_stream(pool, j, S(stream));
+    BBH_TRY(call.use(j, st));
     bbh_workspace* w = pool->ws[j];
     segs.clear();
     tok.clear();
@@ -1340,11 +1365,11 @@ bbh_status bbh_embed_batches(bbh_pool* pool, const bbh_model* m, const int32_t* 
     }
     bool ln_deferred = false;  // a pool's workspaces are its own
     BBH_TRY(run_encode_segs(w, m, ids, types, tok.data(), segs.data(), (int)segs.size(),
-                            w->attn_out, pool->streams[j], pool->timer, &ln_deferred));
+                            w->attn_out, st, pool->timer, &ln_deferred));
     for (size_t k = 0; k < segs.size(); ++k) {
       const int i = runs[groups[g].runs[k]].first;
       f16* out = static_cast<f16*>(emb) + emb_rows[i] * BBH_HIDDEN;
-      BBH_TRY(pool_out(pool->timer, pool->streams[j], m, ln_deferred,
+      BBH_TRY(pool_out(pool->timer, st, m, ln_deferred,
                        w->attn_out + segs[k].row * BBH_HIDDEN, segs[k].mask, out, segs[k].batch,
                        segs[k].seq));
     }
@@ -1361,7 +1386,7 @@ bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids
     return fail(BBH_ERR_INVALID_ARG, "bbh_embed_each: null argument");
   if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
   if (!aligned(emb, 4)) return misaligned("bbh_embed_each emb");
-  const int n = (int)pool->streams.size();
+  const int n = pool->n_slots;
   for (int i = 0; i < n_batches; ++i) {
     bbh_status st = check_shape(pool->ws[0], batch_sizes[i], seqs[i]);
     if (st != BBH_OK) return fail(st, "batch " + std::to_string(i) + ": " + g_err);
@@ -1378,22 +1403,15 @@ bbh_status bbh_embed_each(bbh_pool* pool, const bbh_model* m, const int32_t* ids
     load[j] += (size_t)batch_sizes[i] * seqs[i];
   }
   const hipStream_t caller = S(stream);
-  // With two or more slots the last one runs on the caller's stream itself:
-  // its hardware queue would otherwise only wait.  HIP gives a process
-  // GPU_MAX_HW_QUEUES hardware queues (4 by default), so a pool of 4 slots
-  // keeps every queue running a forward (varlen mix: 5.07 -> 4.33 ms a pass
-  // against 3 pool streams beside an idle caller; 2 pool streams + the
-  // caller's run like 3 pool streams).
-  auto slot_stream = [&](int j) { return n > 1 && j == n - 1 ? caller : pool->streams[j]; };
   PoolCall call(pool, caller);
   BBH_TRY(call.begin());
   const int used = n_batches < n ? n_batches : n;  // every batch so far went to an empty stream
-  for (int j = 0; j < used; ++j) BBH_TRY(call.use(j, slot_stream(j)));
+  for (int j = 0; j < used; ++j) BBH_TRY(call.use(j, slot_stream(pool, j, caller)));
   auto one = [&](int i) -> bbh_status {
     if (i == pool->fail_at)
       return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: batch " + std::to_string(i));
     const int j = stream_of[i];
-    const hipStream_t st = slot_stream(j);
+    const hipStream_t st = slot_stream(pool, j, caller);
     bbh_workspace* w = pool->ws[j];
     const int32_t* mk = mask + tok_offsets[i];
     bool ln_deferred = false;  // a pool's workspaces are its own
@@ -1444,7 +1462,7 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
     return fail(BBH_ERR_INVALID_ARG, "bbh_embed_packed: null argument");
   if (n_batches < 0) return fail(BBH_ERR_INVALID_ARG, "n_batches must be >= 0");
   if (!aligned(emb, 4)) return misaligned("bbh_embed_packed emb");
-  const int n = (int)pool->streams.size();
+  const int n = pool->n_slots;
   const size_t cap = pool->ws[0]->rows;  // tokens and sentences per forward
   // The sentences in batch order, validated before anything is enqueued.
   std::vector<bbh::PackedSentence> all;
@@ -1520,7 +1538,7 @@ bbh_status bbh_embed_packed(bbh_pool* pool, const bbh_model* m, const int32_t* i
     if (f == pool->fail_at)
       return fail(BBH_ERR_INVALID_ARG, "bbh_pool_fail_at: forward " + std::to_string(f));
     const int j = f % n;
-    const hipStream_t st = pool->streams[j];
+    const hipStream_t st = slot_stream(pool, j, S(stream));
     BBH_TRY(call.use(j, st));
     bbh_workspace* w = pool->ws[j];
     const size_t first = cut[f], cnt = cut[f + 1] - cut[f];
@@ -1549,7 +1567,9 @@ bbh_status bbh_pool_timing(bbh_pool* pool, int capacity) {
   if (!pool) return fail(BBH_ERR_INVALID_ARG, "null pool");
   if (capacity < 0 || capacity > (1 << 16))
     return fail(BBH_ERR_INVALID_ARG, "timing capacity must be in [0, 65536]");
+  // the last slot's ops ran on a caller's stream: its workspace event follows them
   for (auto st : pool->streams) BBH_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  for (auto e : pool->ws_free) BBH_HIP(hipEventSynchronize(e), "hipEventSynchronize");
   delete pool->timer;
   pool->timer = nullptr;
   if (capacity == 0) return BBH_OK;
@@ -1576,7 +1596,7 @@ bbh_status bbh_pool_timing_read(bbh_pool* pool, bbh_launch_time* out, int max, i
   if (!pool->timer) return BBH_OK;
   for (auto st : pool->streams) BBH_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
   OpTimer* t = pool->timer;
-  // bbh_embed_each runs one slot on the caller's stream: wait for the events.
+  // The last slot runs on the caller's stream: wait for the events.
   for (int i = 0; i < t->used; ++i)
     BBH_HIP(hipEventSynchronize(t->ev[2 * i + 1]), "hipEventSynchronize");
   for (int i = 0; i < t->used; ++i)

@@ -1023,25 +1023,29 @@ const char* tile_name(int id) {
 // large M run on the weight-resident kernel instead (wres_ok).  Small M wants
 // many small tiles (latency, CU coverage); large M wants big tiles (L2 and
 // LDS traffic per MFMA).  From 1025 to 4096 rows (the batch-64 forwards of
-// the length buckets) the choice comes from the concurrent per-batch pass,
-// where the kernels of other forwards share the CUs, rather than from one
-// kernel alone: every tile tried for each (shape, M) with the others fixed,
-// then the winners confirmed in interleaved repeats.  FFN1 takes the 128x128
-// register-staged tile (30) from 1025 rows and FFN2 the 64x128 copy-ring
-// tile (1) from 2049 rows: 391K -> 409K sentences/s for the pass on three
-// streams; a sweep on four found no tile ahead of these.  Fewer, larger
-// tiles move fewer bytes L2 -> CU per FLOP.
-int pick_plain(int M, int N, int K) {
+// the length buckets) the best tile depends on whether other forwards share
+// the CUs.  Alone (shared false: bbh_embed, a one-slot pool) FFN1 keeps the
+// 64x64 copy-ring tile (0) to 2048 rows and the 64x64 register-staged one
+// (26) to 3072, and FFN2 the 64x64 copy ring: more workgroups than CUs keep
+// every CU busy.  Beside other forwards (shared true: a pool of several
+// slots) every tile was tried for each (shape, M) with the others fixed in
+// the per-batch pass, then the winners confirmed in interleaved repeats:
+// FFN1 takes the 128x128 register-staged tile (30) from 1025 rows and FFN2
+// the 64x128 copy-ring tile (1) from 2049 rows, 391K -> 409K sentences/s for
+// the pass on three streams; a sweep on four found no tile ahead of these.
+// There the other forwards fill the CUs and fewer, larger tiles move fewer
+// bytes L2 -> CU per FLOP.
+int pick_plain(int M, int N, int K, bool shared) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
   if (M <= 1024)
     id = qkv ? 30 : ffn1 ? 0 : 26;
   else if (M <= 2048)
-    id = qkv ? 30 : ffn1 ? 30 : 26;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? 30 : wide_k ? 1 : 0;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : (shared && wide_k) ? 1 : 0;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : wide_k ? 1 : 0;
+    id = qkv ? 32 : ffn1 ? 30 : (shared && wide_k) ? 1 : 0;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)
@@ -1059,9 +1063,9 @@ int pick_plain(int M, int N, int K) {
 
 bool gemm_mfma_ok(int N, int K) { return N % 64 == 0 && K % 64 == 0; }
 
-int gemm_tile(int M, int N, int K) {
+int gemm_tile(int M, int N, int K, bool shared) {
   if (!gemm_mfma_ok(N, K)) return -1;
-  return wres_ok(M, N, K) ? kTiles : pick_plain(M, N, K);
+  return wres_ok(M, N, K) ? kTiles : pick_plain(M, N, K, shared);
 }
 
 // Large M: one kernel whose 128x384 tile owns whole rows.  Smaller M: a tile
@@ -1071,9 +1075,9 @@ int gemm_tile(int M, int N, int K) {
 // The weight-resident kernel takes the K = 384 LayerNorm Linear (O-proj)
 // from M = 65536, where it passes tile 28 (89.5 vs 98.0 us at M = 131072;
 // at M = 26857 its fixed W prologue leaves it 15% behind).
-int gemm_residual_ln_tile(int M, int K, bool* fused_ln) {
+int gemm_residual_ln_tile(int M, int K, bool* fused_ln, bool shared) {
   *fused_ln = M > 8192;
-  if (!*fused_ln) return pick_plain(M, kHidden, K);
+  if (!*fused_ln) return pick_plain(M, kHidden, K, shared);
   if (K == wres::K && M >= 65536) return kTiles;
   return M <= 16384 ? 14 : K >= 1024 ? 18 : 28;
 }
@@ -1085,7 +1089,7 @@ const char* gemm_tile_name(int tile) {
 }
 
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N, int K,
-                Act act, hipStream_t s) {
+                Act act, hipStream_t s, bool shared) {
   const bool gelu = act == Act::kGelu;
   const bool aligned = (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C) & 15) == 0 &&
                        ((uintptr_t)bias & 7) == 0;
@@ -1097,29 +1101,29 @@ hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int 
   }
   if (wres_ok(M, N, K))
     return gelu ? launch_wres<kGelu>(A, W, bias, C, M, N, s) : launch_wres<kBias>(A, W, bias, C, M, N, s);
-  const int id = pick_plain(M, N, K);
+  const int id = pick_plain(M, N, K, shared);
   return gelu ? launch_id<kGelu>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s)
               : launch_id<kBias>(id, A, W, bias, nullptr, nullptr, nullptr, C, M, N, K, 0.f, s);
 }
 
 hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f16* residual,
                             const f16* gamma, const f16* beta, f16* y, int M, int K, float eps,
-                            hipStream_t s) {
+                            hipStream_t s, bool shared) {
   bool fused;
-  const int id = gemm_residual_ln_tile(M, K, &fused);
+  const int id = gemm_residual_ln_tile(M, K, &fused, shared);
   if (id == kTiles)
     return launch_wres<kLayerNorm>(A, W, bias, y, M, kHidden, s, residual, gamma, beta, eps);
   if (fused)
     return launch_id<kLayerNorm>(id, A, W, bias, residual, gamma, beta, y, M, kHidden, K, eps, s);
-  hipError_t e = gemm_residual(A, W, bias, residual, y, M, K, s);
+  hipError_t e = gemm_residual(A, W, bias, residual, y, M, K, s, shared);
   if (e != hipSuccess) return e;
   return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);
 }
 
 hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,
-                         int M, int K, hipStream_t s) {
+                         int M, int K, hipStream_t s, bool shared) {
   bool fused;
-  const int id = gemm_residual_ln_tile(M, K, &fused);
+  const int id = gemm_residual_ln_tile(M, K, &fused, shared);
   if (fused) return hipErrorInvalidValue;
   return launch_id<kResidual>(id, A, W, bias, residual, nullptr, nullptr, y, M, kHidden, K, 0.f, s);
 }

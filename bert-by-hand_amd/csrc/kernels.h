@@ -21,28 +21,32 @@ struct PackedSentence {
 
 // C(M,N) = A(M,K) . W(N,K)^T [+ bias] [GELU].  True when the MFMA path takes
 // the shape (N % 64 == 0, K % 64 == 0); otherwise the plain tiled kernel runs.
+// `shared` (here and below): other forwards run beside this one on the GPU
+// (a pool of several slots), which changes the best tile from 1025 to 4096
+// rows; the result is the same either way.
 bool gemm_mfma_ok(int N, int K);
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N,
-                int K, Act act, hipStream_t s);
+                int K, Act act, hipStream_t s, bool shared = false);
 
 // Tile configuration gemm() / gemm_residual_ln() launch for a shape (-1: the
 // plain tiled kernel), whether the LayerNorm is inside the GEMM kernel, and
 // the configuration's name as it appears in the kernel symbol.
-int gemm_tile(int M, int N, int K);
-int gemm_residual_ln_tile(int M, int K, bool* fused_ln);
+int gemm_tile(int M, int N, int K, bool shared = false);
+int gemm_residual_ln_tile(int M, int K, bool* fused_ln, bool shared = false);
 const char* gemm_tile_name(int tile);
 
 // y(M,384) = LN(A(M,K) . W(384,K)^T + bias + residual) * gamma + beta.
 // y may alias residual.  K % 64 == 0.
 hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias,
                             const f16* residual, const f16* gamma, const f16* beta,
-                            f16* y, int M, int K, float eps, hipStream_t s);
+                            f16* y, int M, int K, float eps, hipStream_t s,
+                            bool shared = false);
 
 // The first half of gemm_residual_ln where gemm_residual_ln_tile says the
 // LayerNorm is not fused: y = A . W^T + bias + residual (fp16), which a
 // layernorm(y, ...) pass then normalises in place.
 hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,
-                         int M, int K, hipStream_t s);
+                         int M, int K, hipStream_t s, bool shared = false);
 
 // The whole feed-forward block in one kernel for M >= ffn_fused_ok's bound:
 // out(M,384) = LN(GELU(X . W1^T + b1) . W2^T + b2 + X) * gamma + beta, with the

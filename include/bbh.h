@@ -166,10 +166,14 @@ bbh_status bbh_graph_launch(bbh_graph *g, bbh_stream_t stream);
 bbh_status bbh_graph_free(bbh_graph *g);
 
 /* ---- many batches ---------------------------------------------------------
- * A pool of n_streams HIP streams (default priority), each with its own
- * workspace of (max_batch, max_seq).  bbh_embed_batches runs bert_embed on
- * n_batches batches spread over the pool streams so that independent batches
- * overlap on the GPU; it replaces the reference's
+ * A pool of n_streams slots, each with its own workspace of (max_batch,
+ * max_seq).  The last slot runs on the stream a call is made on, the others
+ * on n_streams - 1 HIP streams of the pool (default priority); a one-slot pool
+ * thus runs on the caller's stream alone.  From 2 slots the GEMMs of a forward
+ * use tiles chosen for a GPU shared with other forwards (the same results).
+ * bbh_embed_batches runs bert_embed on n_batches batches spread over the
+ * slots so that independent batches overlap on the GPU; it replaces the
+ * reference's
  * sequential corpus loop (bench/corpus.cu:64-77,120-132).  Batch i reads its
  * (batch_sizes[i], seqs[i]) ids/types/mask starting at element
  * tok_offsets[i] of the device arrays and writes batch_sizes[i] rows of emb
@@ -186,9 +190,9 @@ bbh_status bbh_graph_free(bbh_graph *g);
  * alone: bit for bit while its LayerNorm path is the one a lone batch takes,
  * else to within the rounding of the LayerNorm row statistics (larger groups
  * fuse the LayerNorm into the GEMM epilogue).  Groups are formed largest run
- * first, one per stream while streams remain, then into the group with the
+ * first, one per slot while slots remain, then into the group with the
  * fewest rows that has room; they go largest first to the least-loaded
- * stream.  The call orders itself after prior work on `stream` and makes
+ * slot.  The call orders itself after prior work on `stream` and makes
  * later work on `stream` wait for all batches; it returns without a host
  * sync.  On every return, errors included, everything the call enqueued is
  * ordered before later work on `stream`, so a caller may free emb or the
@@ -203,8 +207,8 @@ bbh_status bbh_graph_free(bbh_graph *g);
 typedef struct bbh_pool bbh_pool;
 bbh_status bbh_pool_create(int n_streams, int max_batch, int max_seq, bbh_pool **out);
 bbh_status bbh_pool_free(bbh_pool *pool);
-/* Number of pool streams, plus workspaces last used on a caller's stream,
- * with work still pending (0 when the pool is idle).  No counterpart in the
+/* Number of pool streams, plus workspaces last used on any stream, with
+ * work still pending (0 when the pool is idle).  No counterpart in the
  * reference: for callers that poll instead of synchronising. */
 bbh_status bbh_pool_busy(bbh_pool *pool, int *busy);
 /* Test hook, no counterpart in the reference: later calls on this pool fail
@@ -225,15 +229,14 @@ bbh_status bbh_embed_batches(bbh_pool *pool, const bbh_model *m, const int32_t *
  * forward at its own (batch_sizes[i], seqs[i]) shape: nothing is merged and
  * every padding row is computed, so each batch's embeddings are bit for bit
  * those of bbh_embed on that batch.  Batch i goes, in batch order, to the
- * slot with the fewest rows so far.  A pool of n >= 2 slots runs slots
- * 0 .. n-2 on its own streams and slot n-1 on `stream` itself, so n = 4 keeps
- * HIP's 4 hardware queues per process (GPU_MAX_HW_QUEUES) busy; one slot
- * runs on the pool's stream.  The call orders itself after prior work on
- * `stream`, makes later work on `stream` wait for all batches, and returns
- * without a host sync.  With more than one stream in use (and op
- * timing off) each stream's launches are enqueued by a host thread of its
- * own: the caller's thread for slot 0, the pool's threads (created with the
- * pool, on the pool's device) for the others. */
+ * slot with the fewest rows so far.  Slots 0 .. n-2 run on the pool's
+ * streams and slot n-1 on `stream` itself, so n = 4 keeps HIP's 4 hardware
+ * queues per process (GPU_MAX_HW_QUEUES) busy.  The call orders itself after
+ * prior work on `stream`, makes later work on `stream` wait for all batches,
+ * and returns without a host sync.  With more than one slot in use (and op
+ * timing off) each slot's launches are enqueued by a host thread of its own:
+ * the caller's thread for slot 0, the pool's threads (created with the pool,
+ * on the pool's device) for the others. */
 bbh_status bbh_embed_each(bbh_pool *pool, const bbh_model *m, const int32_t *ids,
                           const int32_t *types, const int32_t *mask,
                           const int64_t *tok_offsets, const int *batch_sizes, const int *seqs,
@@ -254,7 +257,7 @@ bbh_status bbh_embed_each(bbh_pool *pool, const bbh_model *m, const int32_t *ids
  * both forwards take the same LayerNorm path (a forward of more than 8192
  * rows fuses it into the GEMM epilogue), else to within the rounding of the
  * LayerNorm row statistics.  A sentence of length 0 gets a zero embedding.
- * Sentences are split, in order, into one forward per pool stream of about
+ * Sentences are split, in order, into one forward per slot of about
  * equal token counts (more if a forward would exceed a workspace's
  * max_batch*max_seq tokens or sentences); seqs need not be multiples of 16.
  * A sentence longer than a workspace's max_batch*max_seq rows is rejected
@@ -274,9 +277,9 @@ bbh_status bbh_embed_packed(bbh_pool *pool, const bbh_model *m, const int32_t *i
  * bbh_embed_packed launch (the
  * reference times whole forwards with CUDA events, src/core/timer.h:36-39).
  * bbh_pool_timing(pool, capacity) starts a new record: a pair of events goes
- * on the launching pool stream around every op of every forward, for the
+ * on the launching stream around every op of every forward, for the
  * first `capacity` ops (later ones run untimed).  capacity 0 stops timing and
- * releases the events.  bbh_pool_timing_read waits for the pool streams, then
+ * releases the events.  bbh_pool_timing_read waits for the recorded events, then
  * copies up to `max` records in launch order and sets *count to the number
  * recorded. */
 typedef enum bbh_op {

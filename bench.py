@@ -11,9 +11,13 @@ concurrent HIP streams (the pool's and the caller's), one workspace each.  value
 timed steps, inputs pre-uploaded to HBM.
 
 The roofline names the dominant kernel class of that pass: the same pass on a
-one-stream pool with a pair of HIP events around every launch on that stream
-(so no other stream shares the GPU during a launch); achieved = algorithmic
-FLOPs (GEMMs, attention) or bytes (row kernels) per launch / mean launch time.
+one-slot pool with a pair of HIP events around every launch on the caller's
+stream (so no other stream shares the GPU during a launch).  Its bound is the
+roof that binds at the kernel's arithmetic intensity (FLOPs over the measured
+L2-miss bytes of a counter run where one is committed, else over the
+algorithmic bytes) against the ridge PEAK_FP16_DENSE / PEAK_HBM: MFMA above
+it, HBM below; achieved = algorithmic FLOPs or bytes per launch / mean launch
+time, in that roof's unit, and frac_of_mfma_peak is given either way.
 
 Extra fields: the same pass on one stream; the reference corpus benchmark's
 two modes on the same sentences (length-sorted dynamic batches, and every
@@ -303,6 +307,24 @@ def short_kernel(name):
     return m.group(1) if m else n[:60]
 
 
+def tile_id(kernel_class):
+    """The GEMM tile configuration id of a short_kernel class (the id that
+    bbh_gemm_tile_name names; 33 = the weight-resident kernel), else ""."""
+    import re
+
+    if kernel_class.startswith("gemm_wres_kernel"):
+        return "33"
+    m = re.search(r"(Cfg<[\d,]+>)", kernel_class)
+    if not m:
+        return ""
+    from bbh import capi
+
+    for i in range(64):
+        if capi.lib().bbh_gemm_tile_name(i).decode() == m.group(1):
+            return str(i)
+    return "?"
+
+
 def op_tags(rows, queue_col, grid):
     """Dispatch_Id -> " [o_proj]" / " [ffn2]" for the residual GEMMs of
     profiler rows.  O-proj and FFN2 can run the same kernel on the same grid
@@ -333,9 +355,11 @@ def op_tags(rows, queue_col, grid):
 def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None):
     """Per (kernel class, grid size) means over the dispatches of rocprofv3
     --pmc counter_collection CSVs, as a markdown table.  FETCH_SIZE and
-    WRITE_SIZE (KiB) are turned into bytes with the copy-calibration scales;
-    with a --kernel-trace CSV, the mean duration (dispatches on `stream` only,
-    if given) and the HBM rate (fetch + write) / duration are added."""
+    WRITE_SIZE (KiB) are turned into bytes with the copy-calibration scales:
+    bytes that miss the L2 (what HBM and the memory-side cache serve, an upper
+    bound on HBM traffic); with a --kernel-trace CSV, the mean duration
+    (dispatches on `stream` only, if given) and the L2-miss rate
+    (fetch + write) / duration are added."""
     import csv
 
     acc, counters = {}, []
@@ -360,10 +384,10 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
                            []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     mean = lambda v: sum(v) / len(v)  # noqa: E731
     cols = [c for c in counters if c not in ("FETCH_SIZE", "WRITE_SIZE")]
-    head = ["kernel", "grid (work-items)", "dispatches"]
+    head = ["kernel", "tile", "grid (work-items)", "dispatches"]
     if trace:
         head += ["mean us (trace)"]
-    head += ["HBM read MB", "HBM write MB"] + (["HBM GB/s"] if trace else []) + cols
+    head += ["L2-miss read MB", "L2-miss write MB"] + (["L2-miss GB/s"] if trace else []) + cols
     lines = ["| " + " | ".join(head) + " |", "|---|" + "---:|" * (len(head) - 1)]
     rows = []
     for (k, g), d in sorted(acc.items()):
@@ -371,7 +395,7 @@ def pmc_summary(paths, trace=None, fetch_scale=1.0, write_scale=1.0, stream=None
         rd = mean(d["FETCH_SIZE"].values()) * 1024 * fetch_scale if "FETCH_SIZE" in d else None
         wr = mean(d["WRITE_SIZE"].values()) * 1024 * write_scale if "WRITE_SIZE" in d else None
         us = mean(dur[(k, g)]) if (k, g) in dur else None
-        cells = [f"`{k}`", f"{g:,}", str(n)]
+        cells = [f"`{k}`", tile_id(k), f"{g:,}", str(n)]
         if trace:
             cells.append(f"{us:.2f}" if us else "")
         cells += [f"{rd / 1e6:.2f}" if rd is not None else "", f"{wr / 1e6:.2f}" if wr is not None else ""]
@@ -410,6 +434,35 @@ def trace_summary(trace, stream):
         lines.append(f"| `{k}` | {g:,} | {c['n']} | {mean(c['own'])} | {mean(c['other'])} | "
                      f"{100 * c['sum'] / total:.1f} |")
     return "\n".join(lines)
+
+
+# (tile id, M, N, K, epilogue): a shape at which bbh_linear (epilogue "bias" /
+# "gelu") or bbh_linear_residual_layernorm ("ln") launches that tile, for the
+# tile configurations the forwards pick (1 is picked only beside other
+# forwards: the per-batch pass on several slots).
+TILE_SHAPES = [(0, 1024, 1536, 384, "gelu"), (26, 1024, 384, 384, "bias"),
+               (30, 1024, 1152, 384, "bias"), (31, 8192, 384, 1536, "bias"),
+               (32, 16384, 384, 1536, "bias"), (19, 32768, 384, 1536, "bias"),
+               (14, 16384, 384, 1536, "ln"),
+               (28, 32768, 384, 384, "ln"), (18, 32768, 384, 1536, "ln"),
+               (33, 32768, 1152, 384, "bias")]
+
+
+def run_tiles(torch, engine, steps, warmup):
+    """Each TILE_SHAPES launch, timed alone: {"tile M N K epi": us}."""
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    h = lambda *shape: (torch.randn(*shape, device="cuda", generator=gen) * 0.5).half()  # noqa: E731
+    out = {}
+    for tile, M, N, K, epi in TILE_SHAPES:
+        A, W, b = h(M, K), h(N, K), h(N)
+        C = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        if epi == "ln":
+            r, g, be = h(M, N), torch.ones(N, dtype=torch.float16, device="cuda"), h(N)
+            fn = lambda: engine.launch_linear_residual_layernorm(A, W, b, r, g, be, C, M, K)  # noqa: E731,E501
+        else:
+            fn = lambda: engine.launch_matmul(A, W, C, M, N, K, bias=b, gelu=epi == "gelu")  # noqa: E731
+        out[f"{tile} {M}x{N}x{K} {epi}"] = round(timed(torch, fn, steps, warmup) * 1e3, 2)
+    return out
 
 
 def run_cfg5(torch, engine, synth, model, ws):
@@ -470,8 +523,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only time a device-to-device copy of BYTES (the calibration kernel "
-                         "for the HBM byte counters, and the practical copy bandwidth)")
-    ap.add_argument("--only", choices=["varlen", "cfg2", "cfg3", "cfg5"], default=None,
+                         "for the L2-miss byte counters, and the practical copy bandwidth)")
+    ap.add_argument("--only", choices=["varlen", "varlen1", "packed", "merged", "cfg2", "cfg3",
+                                       "cfg5", "tiles"],
+                    default=None,
                     help="only this workload, without the event-timed roofline pass (for "
                          "rocprofv3 counter runs); prints its dict")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV", default=None,
@@ -488,7 +543,7 @@ def main():
                     help="with --pmc-summary: bytes per reported FETCH_SIZE / WRITE_SIZE byte, "
                          "from the same counters on the --copy-probe copy")
     ap.add_argument("--traffic-json", metavar="OUT", default=None,
-                    help="with --pmc-summary: also write each kernel class's HBM bytes per "
+                    help="with --pmc-summary: also write each kernel class's L2-miss bytes per "
                          "dispatch (fetch + write, dispatch-weighted over its grids) to OUT")
     args = ap.parse_args()
     if args.trace_summary:
@@ -534,16 +589,36 @@ def main():
         return
     weights = synth.make_weights(0)
     model = engine.Model.from_weights(weights)
-    if args.only == "varlen":  # the default workload's pass alone
+    if args.only in ("varlen", "varlen1"):  # the default workload's pass alone (varlen1: the
+        # one-slot pass whose launches the roofline times)
+        slots = EACH_STREAMS if args.only == "varlen" else 1
         batches = synth.varlen_mix()
         pk = engine.PackedBatches([b[:3] for b in batches])
         emb_all = torch.empty((pk.rows, 384), dtype=torch.float16, device="cuda")
-        pool = engine.Pool(EACH_STREAMS, 64, 64)
+        pool = engine.Pool(slots, 64, 64)
         ms, _ = pass_timer(torch, lambda: engine.embed_each(pool, model, pk, emb=emb_all),
                            args.steps, args.warmup)
         pool.close()
         model.close()
-        print(json.dumps({"workload": "varlen per-batch pass", "streams": EACH_STREAMS,
+        print(json.dumps({"workload": "varlen per-batch pass", "streams": slots,
+                          "ms_per_pass": round(ms, 4), "sentences_per_s": round(2000 / (ms / 1e3), 1)}),
+              flush=True)
+        return
+    if args.only == "tiles":  # one kernel-level launch per tile configuration the product picks
+        print(json.dumps(run_tiles(torch, engine, args.steps, args.warmup)), flush=True)
+        model.close()
+        return
+    if args.only in ("packed", "merged"):  # the varlen mix through bbh_embed_packed / _batches
+        batches = synth.varlen_mix()
+        pkg = engine.PackedBatches([b[:3] for b in batches], group_by_seq=True)
+        emb_all = torch.empty((pkg.rows, 384), dtype=torch.float16, device="cuda")
+        ppool = engine.Pool(1, POOL_BATCH, 64)
+        run = engine.embed_packed if args.only == "packed" else engine.embed_batches
+        ms, _ = pass_timer(torch, lambda: run(ppool, model, pkg, emb=emb_all), args.steps,
+                           args.warmup)
+        ppool.close()
+        model.close()
+        print(json.dumps({"workload": f"varlen mix, bbh_embed_{'packed' if args.only == 'packed' else 'batches'}",
                           "ms_per_pass": round(ms, 4), "sentences_per_s": round(2000 / (ms / 1e3), 1)}),
               flush=True)
         return
@@ -638,12 +713,9 @@ def main():
     pool1.timing(0)
     classes = classify(engine, recs, tsteps)
     dom = classes[0]
-    gemm = not dom["op"] in ("embed", "pool", "layernorm")
-    ach = dom["tflops"] if gemm else dom["gb_per_s"]
-    peak = PEAK_FP16_DENSE / 1e12 if gemm else PEAK_HBM / 1e9
     traffic = None
     tfile = os.path.join(PROFILES, "dominant_kernel_traffic.json")
-    if os.path.exists(tfile):  # HBM bytes per dispatch of each class in a --pmc run of this pass
+    if os.path.exists(tfile):  # L2-miss bytes per dispatch of each class in a --pmc run of this pass
         # Residual GEMM rows carry the op (op_tags): O-proj and FFN2 may share
         # kernel and grid.
         tag = {"o_proj_ln": " [o_proj]", "ffn2_ln": " [ffn2]"}.get(dom["op"], "")
@@ -652,9 +724,21 @@ def main():
             for t in json.load(open(tfile)).get("kernels", []):
                 if traffic is None and t.get("class") == name and g in t.get("grid_bytes", {}):
                     traffic = t["grid_bytes"][g]
+    # The roof that binds: the kernel's arithmetic intensity (FLOPs over the
+    # measured L2-miss bytes where a counter run gave them, else over the
+    # algorithmic bytes) against the ridge point PEAK_FP16_DENSE / PEAK_HBM.
+    flops, byts = dom["algorithmic_flops_per_launch"], dom["algorithmic_bytes_per_launch"]
+    ai = flops / (traffic or byts)
+    ridge = PEAK_FP16_DENSE / PEAK_HBM
+    gemm = ai >= ridge
+    ach = dom["tflops"] if gemm else dom["gb_per_s"]
+    peak = PEAK_FP16_DENSE / 1e12 if gemm else PEAK_HBM / 1e9
     out["roofline"] = {
         "bound": "mfma" if gemm else "hbm", "achieved": ach, "peak": peak,
         "unit": "TFLOP/s" if gemm else "GB/s", "frac": round(ach / peak, 4), "traffic": traffic,
+        "flop_per_byte": round(ai, 1), "ridge_flop_per_byte": round(ridge, 1),
+        "attainable_tflops": round(min(PEAK_FP16_DENSE, ai * PEAK_HBM) / 1e12, 1),
+        "frac_of_mfma_peak": round(dom["tflops"] / (PEAK_FP16_DENSE / 1e12), 4),
         "kernel": dom["kernel"], "op": dom["op"], "m": dom["m"], "grid_items": dom["grid_items"],
         "launches_per_step": dom["launches_per_step"], "avg_launch_us": dom["avg_launch_us"],
         "algorithmic_flops_per_launch": dom["algorithmic_flops_per_launch"],

@@ -286,11 +286,11 @@ def short_kernel(name):
     import re
 
     n = name.replace("(anonymous namespace)::", "").replace("bbh::", "").replace(" ", "")
-    m = (re.search(r"gemm_kernel<Cfg<([\d,]+)>,(\d)>", n) or
-         re.search(r"gemm_kernelINS0_3CfgILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)"
+    m = (re.search(r"gemm_kernel<Cfg<([-\d,]+)>,(\d)>", n) or
+         re.search(r"gemm_kernelINS0_3CfgILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(n?\d+)ELi(\d+)"
                    r"EEELi(\d)E", n))
     if m:
-        g = m.groups()
+        g = [x.replace("n", "-") for x in m.groups()]  # Itanium mangling writes -2 as n2
         cfg, epi = (g[0], g[1]) if len(g) == 2 else (",".join(g[:7]), g[7])
         return f"gemm_kernel<Cfg<{cfg}>, {epi}>"
     m = re.search(r"gemm_wres_kernel(?:<|ILi)(\d)", n)
@@ -314,12 +314,12 @@ def tile_id(kernel_class):
 
     if kernel_class.startswith("gemm_wres_kernel"):
         return "33"
-    m = re.search(r"(Cfg<[\d,]+>)", kernel_class)
+    m = re.search(r"(Cfg<[-\d,]+>)", kernel_class)
     if not m:
         return ""
     from bbh import capi
 
-    for i in range(64):
+    for i in range(64):  # every id the table can hold
         if capi.lib().bbh_gemm_tile_name(i).decode() == m.group(1):
             return str(i)
     return "?"
@@ -441,6 +441,7 @@ def trace_summary(trace, stream):
 # tile configurations the forwards pick (1 is picked only beside other
 # forwards: the per-batch pass on several slots).
 TILE_SHAPES = [(0, 1024, 1536, 384, "gelu"), (26, 1024, 384, 384, "bias"),
+               (34, 3072, 384, 1536, "bias"),
                (30, 1024, 1152, 384, "bias"), (31, 8192, 384, 1536, "bias"),
                (32, 16384, 384, 1536, "bias"), (19, 32768, 384, 1536, "bias"),
                (14, 16384, 384, 1536, "ln"),

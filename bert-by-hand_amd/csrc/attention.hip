@@ -204,13 +204,18 @@ __global__ __launch_bounds__(64 * NW, T == 2 ? 4 : 6) void attention_kernel(
       bool up = false;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        float v = fmaxf(fmaxf(s[t][0], s[t][1]), s[t][2]);
+        // IEEE maximum (v_maximum3_f32): scores hold no NaN, and unlike fmaxf
+        // it needs no canonicalising v_max_f32 of each MFMA result first.
+        float v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[t][0], s[t][1]),
+                                                s[t][2]);
 #pragma unroll
-        for (int i = 3; i < 15; i += 2) v = fmaxf(fmaxf(v, s[t][i]), s[t][i + 1]);
-        v = fmaxf(v, s[t][15]);
+        for (int i = 3; i < 15; i += 2)
+          v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(v, s[t][i]), s[t][i + 1]);
+        v = __builtin_elementwise_maximum(v, s[t][15]);
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
                                                          false, false);
-        mx[t] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // finite: a key is unmasked
+        mx[t] = __builtin_elementwise_maximum(__uint_as_float(sw[0]),
+                                              __uint_as_float(sw[1]));  // finite: a key is unmasked
         up = up || mx[t] > m[t] + lag;
       }
       if (!started) {

@@ -45,7 +45,10 @@ enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
 template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0, int SW_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, SA = SA_, SW = SW_, BK = 64;
-  static constexpr int PD = PD_;  // > 0: register prefetch depth (mainloop_reg)
+  // PD_ > 0: register prefetch depth (mainloop_reg); PD_ < 0: the copy-ring
+  // loop with KPB = -PD_ K slices per barrier (mainloop_multi).
+  static constexpr int PD = PD_ > 0 ? PD_ : 0;
+  static constexpr int KPB = PD_ < 0 ? -PD_ : 1;
   using L = Slice<64>;
   static constexpr int NW = WM * WN, THREADS = 64 * NW;  // 4 or 8 wavefronts
   static constexpr int TM = BM / WM, TN = BN / WN;  // wave tile
@@ -67,6 +70,8 @@ struct Cfg {
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is whole 32x32 blocks");
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load distribution");
   static_assert(SA >= 2 && SW >= 2, "ring depths");
+  static_assert(KPB == 1 || (PD == 0 && SA == 2 * KPB && SW == 2 * KPB),
+                "KPB slices per barrier: rings of 2 * KPB slices");
   // vmcnt that may stay outstanding when slice kt must have landed: the
   // copies issued after the later of W(kt) and A(kt) (W is issued first in
   // each iteration).
@@ -222,6 +227,57 @@ __device__ __forceinline__ void mainloop(const f16* __restrict__ A, const f16* _
     const f16* sA = ringA + (kt % C::SA) * C::A_STAGE;
     const f16* sW = ringW + (kt % C::SW) * C::W_STAGE;
     compute_slice<C>(sA, sW, acc);
+  }
+  lds_barrier();  // ring free for the epilogue
+}
+
+// The copy-ring K loop with KPB slices per barrier: rings of 2 * KPB slices
+// for A and W.  Iteration k0 waits for slices k0 .. k0+KPB-1 (the copies
+// issued one iteration earlier), passes one barrier, refills the KPB slots
+// that iteration k0-KPB read with slices k0+KPB .., and runs its KPB slices,
+// so the copy wait, the barrier and the copy issue are paid once per KPB
+// slices instead of once per slice.  Same k order and accumulation as
+// mainloop.
+template <class C>
+__device__ __forceinline__ void mainloop_multi(const f16* __restrict__ A,
+                                               const f16* __restrict__ W, int M, int K, int m0,
+                                               int n0, f16* smem, f32x16 (&acc)[C::FM][C::FN]) {
+#pragma unroll
+  for (int fm = 0; fm < C::FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < C::FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[fm][fn][i] = 0.f;
+
+  constexpr int P = C::KPB;
+  const int KT = K / C::BK;
+  f16* ringA = smem;
+  f16* ringW = smem + C::W_BASE;
+  const f16* a0 = A + (size_t)m0 * K;
+  const f16* w0 = W + (size_t)n0 * K;
+  uint32_t offA[C::LA], offW[C::LW];
+  row_offsets<C::BM, C::NW>(K, M - m0, offA);
+  row_offsets<C::BN, C::NW>(K, C::BN, offW);
+  const __amdgpu_buffer_rsrc_t rA = buffer_of(a0, (uint32_t)(M - m0) * K * 2u);
+  const __amdgpu_buffer_rsrc_t rW = buffer_of(w0, (uint32_t)C::BN * K * 2u);
+  auto issue = [&](int s) {
+    issue_rows_at<C::BN, C::NW>(rW, s * C::BK * 2, offW, ringW + (s % C::SW) * C::W_STAGE);
+    issue_rows_at<C::BM, C::NW>(rA, s * C::BK * 2, offA, ringA + (s % C::SA) * C::A_STAGE);
+  };
+#pragma unroll
+  for (int d = 0; d < P; ++d)
+    if (d < KT) issue(d);
+  for (int k0 = 0; k0 < KT; k0 += P) {
+    wait_vm<0>();
+    lds_barrier();  // slices k0 .. k0+P-1 visible to all; k0-P .. k0-1 consumed
+#pragma unroll
+    for (int d = 0; d < P; ++d)
+      if (k0 + P + d < KT) issue(k0 + P + d);
+#pragma unroll
+    for (int d = 0; d < P; ++d)
+      if (k0 + d < KT)
+        compute_slice<C>(ringA + ((k0 + d) % C::SA) * C::A_STAGE,
+                         ringW + ((k0 + d) % C::SW) * C::W_STAGE, acc);
   }
   lds_barrier();  // ring free for the epilogue
 }
@@ -407,6 +463,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   f32x16 acc[C::FM][C::FN];
   if constexpr (C::PD > 0)
     mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
+  else if constexpr (C::KPB > 1)
+    mainloop_multi<C>(A, W, M, K, m0, n0, smem, acc);
   else
     mainloop<C>(A, W, M, K, m0, n0, smem, acc);
 
@@ -915,7 +973,7 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 }
 
 // Tile configurations (BM, BN, wavefronts M x N, A-ring depth), by id; the K
-// slice is 64 wide and the W ring 2 deep throughout.  The product build holds
+// slice is 64 wide and the W ring 2 deep but in tile 34.  The product build holds
 // the configurations pick_plain and gemm_residual_ln_tile choose; the others
 // of the sweep that chose them are compiled only with -DBBH_TUNING.
 //   id  tile      wave tile  SA   LDS
@@ -931,6 +989,8 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 //   30  128x128   64x32 (8w) PD 2   64 KB
 //   31  128x128   32x64 (8w) PD 2   64 KB
 //   32  128x192   32x96 (8w) PD 2   80 KB
+//   copy rings with two K slices per barrier (PD -2; A and W rings 4 deep):
+//   34  64x64     32x32      4/4    64 KB
 // Kernel symbols read gemm_kernel<Cfg<BM,BN,WM,WN,SA,PD,SW>, epilogue>.
 // The table itself: X(id, BM, BN, WM, WN, SA, PD, SW).
 #define BBH_TILES(X) \
@@ -943,7 +1003,8 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
   X(28, 128, 384, 2, 4, 2, 2, 2) \
   X(30, 128, 128, 2, 4, 2, 2, 2) \
   X(31, 128, 128, 4, 2, 2, 2, 2) \
-  X(32, 128, 192, 4, 2, 2, 2, 2)
+  X(32, 128, 192, 4, 2, 2, 2, 2) \
+  X(34, 64, 64, 2, 2, 4, -2, 4)
 
 #ifdef BBH_TUNING
 // The rest of the sweep (ids 2-13, 15-17, 20-25, 27, 29).
@@ -975,7 +1036,7 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 #define BBH_TUNING_TILES(X)
 #endif
 
-constexpr int kTiles = 33;  // ids 0 .. 32; kTiles names the weight-resident kernel
+constexpr int kTiles = 33;  // kTiles names the weight-resident kernel (no tile has this id)
 
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
@@ -1026,8 +1087,10 @@ const char* tile_name(int id) {
 // the length buckets) the best tile depends on whether other forwards share
 // the CUs.  Alone (shared false: bbh_embed, a one-slot pool) FFN1 keeps the
 // 64x64 copy-ring tile (0) to 2048 rows and the 64x64 register-staged one
-// (26) to 3072, and FFN2 the 64x64 copy ring: more workgroups than CUs keep
-// every CU busy.  Beside other forwards (shared true: a pool of several
+// (26) to 3072, and O-proj and FFN2 from 2049 rows run the 64x64 copy ring
+// with two K slices per barrier (34; one-slot varlen pass 9.00-9.03 ->
+// 8.84-8.95 ms): more workgroups than CUs keep every CU busy, and the
+// deeper rings fit beside nothing else.  Beside other forwards (shared true: a pool of several
 // slots) every tile was tried for each (shape, M) with the others fixed in
 // the per-batch pass, then the winners confirmed in interleaved repeats:
 // FFN1 takes the 128x128 register-staged tile (30) from 1025 rows and FFN2
@@ -1043,9 +1106,9 @@ int pick_plain(int M, int N, int K, bool shared) {
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : (shared && wide_k) ? 1 : 0;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : !shared ? 34 : wide_k ? 1 : 0;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : (shared && wide_k) ? 1 : 0;
+    id = qkv ? 32 : ffn1 ? 30 : !shared ? 34 : wide_k ? 1 : 0;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

@@ -61,20 +61,22 @@ def test_linear_rows_identical_across_kernels(torch_cuda, N, gelu):
     # The first rows of a large-M GEMM equal the same rows computed alone:
     # every kernel accumulates in the same k order and rounds the same way.
     # M = 50000 runs QKV and FFN1 on the weight-resident kernel and N = 384 on
-    # a 128x128 tile; M = 2048 runs all three on 64x64 tiles.
+    # a 128x128 tile; M = 2048 runs all three on 64x64 tiles; M = 3000 runs
+    # N = 384 on the 64x64 copy ring with two K slices per barrier (tile 34).
     torch = torch_cuda
     from bbh import engine
 
-    M, K, m = 50000, 384, 2048
+    M, K = 50000, 384
     rng = np.random.default_rng(N + 11)
     A, W, b = _h(rng, (M, K)), _h(rng, (N, K), 1.0 / np.sqrt(K)), _h(rng, (N,), 0.1)
     dA, dW, db = to_dev(torch, A), to_dev(torch, W), to_dev(torch, b)
     big = torch.empty((M, N), dtype=torch.float16, device="cuda")
-    small = torch.empty((m, N), dtype=torch.float16, device="cuda")
     engine.launch_matmul(dA, dW, big, M, N, K, bias=db, gelu=gelu)
-    engine.launch_matmul(dA[:m], dW, small, m, N, K, bias=db, gelu=gelu)
-    torch.cuda.synchronize()
-    assert np.array_equal(_np(big[:m]), _np(small))
+    for m in (2048, 3000):
+        small = torch.empty((m, N), dtype=torch.float16, device="cuda")
+        engine.launch_matmul(dA[:m], dW, small, m, N, K, bias=db, gelu=gelu)
+        torch.cuda.synchronize()
+        assert np.array_equal(_np(big[:m]), _np(small)), m
 
 
 @pytest.mark.parametrize("M", [4096, 32768])

@@ -23,7 +23,8 @@ Extra fields: the same pass on one stream; the reference corpus benchmark's
 two modes on the same sentences (length-sorted dynamic batches, and every
 batch at seq 128, bench/corpus.cu:64-132); the padding-free packed pass and
 the equal-seq-merged padded pass; configs[1] / configs[2] (batch 64 x seq
-16 / 128, 300 iterations as bench/bench.cu:32-51); configs[4] (batch 256 x
+16 / 128, 300 iterations as bench/bench.cu:32-51); the reference's batch
+sweep (batch 1, 8, 32, 64 at seq 128 and 16, bench/bench.cu:86-96); configs[4] (batch 256 x
 seq 512) with the fused GEMMs' fraction of the fp16 dense MFMA peak; the
 tokenizer rate; and the CPU baseline (transformers' BertModel fp32 forward, the
 library the reference's cpu_fp32 leg times, on this host's cores).
@@ -811,6 +812,19 @@ def main():
                         "graph_sentences_per_s": round(64 / (ms_g / 1e3), 1),
                         "graph_ms_per_sentence": round(ms_g / 64, 6)}
             log(tag, out[tag])
+        # ---- the reference's batch sweep (bench/bench.cu:86-96): one 9-token
+        # sentence tiled over batch 1, 8, 32, 64 at seq 128 (padded) and at
+        # its effective length 16, bert_embed 300 times after 20 warmups
+        sweep = {}
+        for seq in (128, 16):
+            for bsz in (1, 8, 32, 64):
+                ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(bsz, seq))
+                ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask,
+                                                            emb=emb[:bsz]), 300, warmup=20)
+                sweep[f"seq{seq}_b{bsz}"] = {"ms_per_sentence": round(ms / bsz, 6),
+                                             "sentences_per_s": round(bsz / (ms / 1e3), 1)}
+        out["batch_sweep"] = sweep
+        log("batch sweep", sweep)
         out["cfg5_b256_s512"] = run_cfg5(torch, engine, synth, model, ws)
         ws.close()
         out["tokenizer"] = tokenizer_rate(engine, synth)

@@ -1083,26 +1083,30 @@ const char* tile_name(int id) {
 // (1536, 384) FFN1, (384, 384) O-proj and (384, 1536) FFN2.  QKV and FFN1 at
 // large M run on the weight-resident kernel instead (wres_ok).  Small M wants
 // many small tiles (latency, CU coverage); large M wants big tiles (L2 and
-// LDS traffic per MFMA).  From 1025 to 4096 rows (the batch-64 forwards of
-// the length buckets) the best tile depends on whether other forwards share
-// the CUs.  Alone (shared false: bbh_embed, a one-slot pool) FFN1 keeps the
-// 64x64 copy-ring tile (0) to 2048 rows and the 64x64 register-staged one
-// (26) to 3072, and O-proj and FFN2 from 2049 rows run the 64x64 copy ring
-// with two K slices per barrier (34; one-slot varlen pass 9.00-9.03 ->
-// 8.84-8.95 ms): more workgroups than CUs keep every CU busy, and the
-// deeper rings fit beside nothing else.  Beside other forwards (shared true: a pool of several
-// slots) every tile was tried for each (shape, M) with the others fixed in
-// the per-batch pass, then the winners confirmed in interleaved repeats:
-// FFN1 takes the 128x128 register-staged tile (30) from 1025 rows and FFN2
-// the 64x128 copy-ring tile (1) from 2049 rows, 391K -> 409K sentences/s for
-// the pass on three streams; a sweep on four found no tile ahead of these.
-// There the other forwards fill the CUs and fewer, larger tiles move fewer
-// bytes L2 -> CU per FLOP.
+// LDS traffic per MFMA).  Up to 4096 rows (the batch-64 forwards of the
+// length buckets) the best tile depends on whether other forwards share the
+// CUs.
+// Alone (shared false: bbh_embed, a one-slot pool), from sweeps of the
+// configs[1] and one-slot configs[3] forwards with one GEMM's tile changed at
+// a time: QKV runs the 64x64 copy-ring tile (0) up to 1024 rows (configs[1]
+// forward 230.1 -> 224.3 us: 288 workgroups instead of 72); FFN1 keeps that
+// tile to 2048 rows and the 64x64 register-staged one (26) to 3072; O-proj
+// and FFN2 from 2049 rows run the 64x64 copy ring with two K slices per
+// barrier (34; one-slot varlen pass 9.00-9.03 -> 8.84-8.95 ms).  More
+// workgroups than CUs keep every CU busy, and the deeper rings fit beside
+// nothing else.
+// Beside other forwards (shared true: a pool of several slots) every tile was
+// tried for each (shape, M) with the others fixed in the per-batch pass, then
+// the winners confirmed in interleaved repeats: FFN1 takes the 128x128
+// register-staged tile (30) from 1025 rows and FFN2 the 64x128 copy-ring tile
+// (1) from 2049 rows, 391K -> 409K sentences/s for the pass on three streams;
+// a sweep on four found no tile ahead of these.  There the other forwards
+// fill the CUs, and fewer, larger tiles move fewer bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K, bool shared) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
   if (M <= 1024)
-    id = qkv ? 30 : ffn1 ? 0 : 26;
+    id = qkv ? (shared ? 30 : 0) : ffn1 ? 0 : 26;
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)

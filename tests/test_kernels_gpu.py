@@ -25,7 +25,8 @@ def _np(t):
 
 GEMM_SHAPES = [
     # (M, N, K, gelu): the four Linears of the path at small / ragged / large M
-    (16, 1152, 384, False), (48, 384, 384, False), (1040, 1536, 384, True),
+    (16, 1152, 384, False), (1000, 1152, 384, False), (48, 384, 384, False),
+    (1040, 1536, 384, True),
     (1024, 384, 1536, False), (3072, 1152, 384, False), (8192, 1536, 384, True),
     (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
     # the batch-64 buckets' tiles, ragged: 128x128 for FFN1, 64x128 for FFN2

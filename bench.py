@@ -821,8 +821,13 @@ def main():
                 ids, types, mask = (torch.from_numpy(a).cuda() for a in synth.cfg_fixed(bsz, seq))
                 ms = timed(torch, lambda: engine.bert_embed(ws, model, ids, types, mask,
                                                             emb=emb[:bsz]), 300, warmup=20)
+                # the same forward captured once as a HIP graph and replayed
+                graph = engine.EmbedGraph(ws, model, ids, types, mask, emb[:bsz])
+                ms_g = timed(torch, graph.launch, 300, warmup=20)
+                graph.close()
                 sweep[f"seq{seq}_b{bsz}"] = {"ms_per_sentence": round(ms / bsz, 6),
-                                             "sentences_per_s": round(bsz / (ms / 1e3), 1)}
+                                             "sentences_per_s": round(bsz / (ms / 1e3), 1),
+                                             "graph_ms_per_sentence": round(ms_g / bsz, 6)}
         out["batch_sweep"] = sweep
         log("batch sweep", sweep)
         out["cfg5_b256_s512"] = run_cfg5(torch, engine, synth, model, ws)

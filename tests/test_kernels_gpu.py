@@ -31,6 +31,8 @@ GEMM_SHAPES = [
     (4096, 384, 1536, False), (100, 128, 64, False), (7, 64, 128, True),
     # the batch-64 buckets' tiles, ragged: 128x128 for FFN1, 64x128 for FFN2
     (2500, 1536, 384, True), (3000, 384, 1536, False),
+    # two K slices per barrier (tile 34) with an odd slice count (3, 1)
+    (3000, 384, 192, False), (2100, 384, 64, True),
     # large-M tiles (cfg5 runs M = 131072 end to end), one shape per tile bucket
     (12288, 1152, 384, False), (16384, 384, 1536, False),
     (32768, 1152, 384, False), (32768, 1536, 384, True), (32768, 384, 384, False),

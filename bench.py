@@ -538,7 +538,7 @@ def main():
                     help="with --pmc-summary: a rocprofv3 kernel_trace CSV for mean durations")
     ap.add_argument("--trace-summary", metavar="CSV", default=None,
                     help="print per-kernel-class times of a rocprofv3 kernel_trace CSV "
-                         "(--trace-stream: the timing pool's Stream_Id) and exit")
+                         "(--trace-stream: the Stream_Id of the pass to single out) and exit")
     ap.add_argument("--trace-stream", default=None,
                     help="with --trace: only dispatches of this Stream_Id")
     ap.add_argument("--scales", nargs=2, type=float, default=(1.0, 1.0), metavar=("FETCH", "WRITE"),

@@ -312,14 +312,15 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
     assert np.abs(h.mean(axis=1)).max() < 0.05  # gamma 1, beta 0 in the seeded weights
 
 
+@pytest.mark.parametrize("slots", [1, 4])
 @pytest.mark.parametrize("entry", ["each", "batches", "packed"])
-def test_pool_error_path_joins_caller_stream(torch_cuda, ws, model, entry):
+def test_pool_error_path_joins_caller_stream(torch_cuda, ws, model, entry, slots):
     # A pool call that fails part-way (the test hook fails batch / group /
-    # forward 3 of bbh_embed_each / _batches / _packed, after the earlier ones
-    # are enqueued on the pool's streams) still orders the caller's stream
-    # after everything it enqueued: once that stream alone is synchronised, no
-    # pool stream has work left.  Every kernel it enqueued runs to the end.
-    # With the hook off, the same pool then gives the sequential results.
+    # forward 3 (1 on one slot) of bbh_embed_each / _batches / _packed, after
+    # the earlier ones are enqueued) still orders the caller's stream after
+    # everything it enqueued: once that stream alone is synchronised, no pool
+    # stream has work left.  Every kernel it enqueued runs to the end.  With
+    # the hook off, the same pool then gives the sequential results.
     from bbh import capi, engine, synth
 
     torch = torch_cuda
@@ -327,9 +328,9 @@ def test_pool_error_path_joins_caller_stream(torch_cuda, ws, model, entry):
     packed = engine.PackedBatches([b[:3] for b in batches])
     run = {"each": engine.embed_each, "batches": engine.embed_batches,
            "packed": engine.embed_packed}[entry]
-    pool = engine.Pool(4, 64, 64)
+    pool = engine.Pool(slots, 64, 64)
     side = torch.cuda.Stream()  # default priority
-    pool.fail_at(3)
+    pool.fail_at(3 if slots > 1 else 1)
     with torch.cuda.stream(side):
         emb = torch.empty((packed.rows, 384), dtype=torch.float16, device="cuda")
         with pytest.raises(capi.BBHError, match="bbh_pool_fail_at"):
@@ -346,11 +347,12 @@ def test_pool_error_path_joins_caller_stream(torch_cuda, ws, model, entry):
     pool.close()
 
 
-def test_pool_calls_from_two_streams_stay_ordered(torch_cuda, ws, model):
-    # bbh_embed_each runs its last slot's workspace on the caller's stream,
-    # bbh_embed_batches and _packed run the same workspace on the pool's own
-    # stream: back-to-back calls on one pool from two caller streams, with no
-    # host sync between them, each give their own batches' embeddings.
+@pytest.mark.parametrize("slots", [1, 4])
+def test_pool_calls_from_two_streams_stay_ordered(torch_cuda, ws, model, slots):
+    # Every pool entry point runs its last slot's workspace on the stream of
+    # the call (a one-slot pool has no stream of its own): back-to-back calls
+    # on one pool from two caller streams, with no host sync between them,
+    # each give their own batches' embeddings.
     from bbh import engine, synth
 
     torch = torch_cuda
@@ -359,7 +361,7 @@ def test_pool_calls_from_two_streams_stay_ordered(torch_cuda, ws, model):
     pa, pb = engine.PackedBatches(a), engine.PackedBatches(b)
     want_a = np.concatenate([_embed(torch, ws, model, *x) for x in a])
     want_b = np.concatenate([_embed(torch, ws, model, *x) for x in b])
-    pool = engine.Pool(4, 64, 64)
+    pool = engine.Pool(slots, 64, 64)
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
     out = []
     for s, fn, pk in [(s1, engine.embed_each, pa), (s2, engine.embed_each, pb),

@@ -73,6 +73,29 @@ def ws(torch_cuda):
     w.close()
 
 
+@pytest.fixture(scope="session")
+def cfg5_oracle(weights32):
+    """configs[4] (256 x 512, lengths 256-512): indices of 32 sentences spread
+    over the lengths, shortest and longest included, and the fp32 oracle's
+    embeddings of them, in four calls of 8 sentences each at the effective
+    length (round16) of the longest of the 8."""
+    from bbh import synth
+    from oracle import bert_oracle as O
+
+    ids, types, mask = synth.long_batch()
+    lens = mask.sum(1)
+    picks = sorted({int(np.argmin(np.abs(lens - t)))
+                    for t in np.linspace(lens.min(), lens.max(), 32)})
+    assert len(picks) >= 28 and lens[picks].min() == lens.min() and lens[picks].max() == lens.max()
+    picks = np.asarray(picks)
+    picks = picks[np.argsort(lens[picks], kind="stable")]
+    want = []
+    for grp in np.array_split(picks, 4):
+        s = synth.round16(int(lens[grp].max()))
+        want.append(O.bert_embed(weights32, ids[grp, :s], types[grp, :s], mask[grp, :s]))
+    return picks, np.concatenate(want)
+
+
 def cosine_rows(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)

@@ -112,6 +112,40 @@ def test_cfg5_long_sequences(torch_cuda, ws, model, weights32, cfg5_oracle):
     assert cosine_rows(got[b:b + 1], own).min() >= COS
 
 
+def test_peaked_attention_end_to_end(torch_cuda, ws, weights32):
+    # The seeded N(0, 0.02) weights give close to uniform attention (scores of
+    # std ~0.15, the largest probability of a row ~1/len).  With the query and
+    # key weights scaled x6 the scores have std ~5.5 in every layer: half the
+    # rows put more than 0.62 of their weight on one key, a tenth more than
+    # 0.95, and the running max of the online softmax moves across key chunks.
+    # Whole forwards on those weights against the oracle on the same weights:
+    # short sentences (seq 64) and long ones (seq 512), padded and packed.
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    w = {k: (v * np.float32(6.0) if k.endswith(("query.weight", "key.weight")) else v)
+         for k, v in weights32.items()}
+    model = engine.Model.from_weights(w)
+    pool = engine.Pool(1, 32, 512)
+    try:
+        rng = np.random.default_rng(21)
+        short = synth.pack([synth.sentence(rng, int(n)) for n in rng.integers(5, 65, size=24)], 64)
+        long = synth.pack([synth.sentence(rng, int(n)) for n in (256, 333, 421, 512)], 512)
+        for ids, types, mask in (short, long):
+            want = O.bert_embed(w, ids, types, mask)
+            got = _embed(torch, ws, model, ids, types, mask)
+            cos = cosine_rows(got, want)
+            assert cos.min() >= COS, (ids.shape, cos.min())
+            pk = engine.PackedBatches([(ids, types, mask)])
+            got_p = _np(engine.embed_packed(pool, model, pk))
+            torch.cuda.synchronize()
+            cos = cosine_rows(got_p, want)
+            assert cos.min() >= COS, ("packed", ids.shape, cos.min())
+    finally:
+        pool.close()
+        model.close()
+
+
 def test_workspace_hidden_is_final_hidden(torch_cuda, ws, model, golden_model):
     from bbh import engine
 

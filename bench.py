@@ -221,6 +221,8 @@ def launch_work(r):
     byts = (M * K + N * K + M * N + N) * 2.0
     if op in ("o_proj_ln", "ffn2_ln"):
         byts += M * N * 2.0  # the residual
+    if r.get("fused_ln") == 2:  # carried LayerNorm: (mean, rstd) a row, and up to 6 tile pairs
+        byts += M * (8.0 + 48.0)
     return flops, byts
 
 
@@ -231,7 +233,11 @@ def kernel_name(engine, op, tile, fused):
            "ffn": "ffn_fused_kernel"}
     if op in row:
         return row[op], row[op]
-    epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else "2 (bias+residual)")
+    if fused == 2:  # the LayerNorm carried between the GEMMs as row statistics
+        epi = {"qkv": "4 (carried LayerNorm in)", "ffn1_gelu": "5 (carried LayerNorm in+GELU)"}.get(
+            op, "6 (bias+residual, row statistics out)")
+    else:
+        epi = EPI_OF_OP.get(op) or ("3 (bias+residual+LayerNorm)" if fused else "2 (bias+residual)")
     tname = engine.gemm_tile_name(tile)
     if tname.startswith("WRes"):
         return f"gemm_wres_kernel<{epi}>", f"gemm_wres_kernel<{epi[0]}>"

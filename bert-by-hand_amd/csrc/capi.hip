@@ -105,17 +105,36 @@ const std::vector<Param>& params() {
 constexpr int kPerLayer = 16;  // state_dict tensors per encoder layer
 constexpr int kEmbParams = 5;
 
-size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+constexpr size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Forwards of up to kCarryMaxRows rows carry their LayerNorms as row
+// statistics (bbh::ln_carry_ok); a workspace holds those statistics for
+// min(rows, kCarryMaxRows) rows: two buffers of tile pairs, two of
+// (mean, rstd).
+constexpr size_t kCarryMaxRows = 8192;
+constexpr size_t carry_rows(size_t rows) { return std::min(rows, kCarryMaxRows); }
+constexpr size_t carry_bytes(size_t rows) {
+  const size_t rc = carry_rows(rows);
+  return 2 * align256(rc * bbh::kMaxCarryTiles * sizeof(float2)) + 2 * align256(rc * sizeof(float2));
+}
 
 }  // namespace
 
 struct bbh_model {
   void* blob = nullptr;
   size_t bytes = 0;
+  void* fold_blob = nullptr;  // the carried-LayerNorm operands (fold_operands)
+  size_t fold_bytes = 0;
   const f16 *word, *pos, *type, *emb_g, *emb_b;
   struct Layer {
     const f16 *qkv_w, *qkv_b, *o_w, *o_b, *ln1_g, *ln1_b;
     const f16 *f1_w, *f1_b, *f2_w, *f2_b, *ln2_g, *ln2_b;
+    // The GEMMs that read rows whose LayerNorm is carried as statistics
+    // (bbh::LnCarry): QKV from layer 1 (the previous layer's ln2) and FFN1
+    // (this layer's ln1): W' = W diag(gamma) (W itself when gamma is all
+    // ones), fs = row sums of W', fc = W . beta + bias.
+    const f16 *qkv_wf = nullptr, *f1_wf = nullptr;
+    const float *qkv_fs = nullptr, *qkv_fc = nullptr, *f1_fs = nullptr, *f1_fc = nullptr;
   } layers[BBH_NUM_LAYERS];
 };
 
@@ -125,6 +144,10 @@ struct bbh_workspace {
   void* blob = nullptr;
   size_t bytes = 0;
   f16 *qkv, *ctx, *attn_out, *inter, *ping, *pong;
+  // Carried LayerNorms (forwards of at most carry_rows rows): tile pairs and
+  // (mean, rstd) of the attention block's (a) and the FFN block's (b) rows.
+  float2 *st_a = nullptr, *st_b = nullptr, *mr_a = nullptr, *mr_b = nullptr;
+  size_t carry_rows = 0;
   bbh::PackedSentence* sents;  // plan of a packed forward: up to `rows` sentences
   bool shared = false;         // a slot of a multi-slot pool: other forwards run beside
 };
@@ -170,6 +193,101 @@ const BlobLayout& layout() {
   return L;
 }
 
+float f16_bits_to_float(uint16_t b) {
+  f16 h;
+  memcpy(&h, &b, sizeof h);
+  return (float)h;
+}
+
+// The carried-LayerNorm operands of every layer (bbh_model::Layer), from the
+// host copy of the weights, into one device allocation: fs and fc in fp32
+// (sums in double), W' = fp16(W * gamma) (the fp32 product of two fp16
+// values is exact, so one rounding) only where gamma is not all ones.
+bbh_status fold_operands(const std::vector<uint16_t>& host, bbh_model* m) {
+  const BlobLayout& L = layout();
+  const size_t H = BBH_HIDDEN;
+  struct Fold {
+    int layer, w, b, g, be;  // param indices: W (N x 384), bias, gamma, beta
+    size_t n;
+    bool qkv;
+  };
+  std::vector<Fold> folds;
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    const int b0 = kEmbParams + i * kPerLayer;
+    if (i > 0) {
+      const int p0 = kEmbParams + (i - 1) * kPerLayer;
+      folds.push_back({i, b0 + 0, b0 + 1, p0 + 14, p0 + 15, 3 * H, true});
+    }
+    folds.push_back({i, b0 + 10, b0 + 11, b0 + 8, b0 + 9, (size_t)BBH_FFN_DIM, false});
+  }
+  // layout: per fold fs | fc (fp32), then W' where needed
+  std::vector<size_t> vec_at(folds.size()), w_at(folds.size(), SIZE_MAX);
+  std::vector<bool> ones(folds.size());
+  size_t cur = 0;
+  for (size_t f = 0; f < folds.size(); ++f) {
+    vec_at[f] = cur;
+    cur = align256(cur + 2 * folds[f].n * sizeof(float));
+  }
+  for (size_t f = 0; f < folds.size(); ++f) {
+    const uint16_t* g = host.data() + L.off[folds[f].g];
+    bool all = true;
+    for (size_t k = 0; k < H; ++k) all = all && g[k] == 0x3C00;  // fp16 1.0
+    ones[f] = all;
+    if (!all) {
+      w_at[f] = cur;
+      cur = align256(cur + folds[f].n * H * sizeof(f16));
+    }
+  }
+  std::vector<unsigned char> buf(cur, 0);
+  for (size_t f = 0; f < folds.size(); ++f) {
+    const Fold& fd = folds[f];
+    const uint16_t* W = host.data() + L.off[fd.w];
+    const uint16_t* bias = host.data() + L.off[fd.b];
+    const uint16_t* g = host.data() + L.off[fd.g];
+    const uint16_t* be = host.data() + L.off[fd.be];
+    float* fs = reinterpret_cast<float*>(buf.data() + vec_at[f]);
+    float* fc = fs + fd.n;
+    f16* wf = ones[f] ? nullptr : reinterpret_cast<f16*>(buf.data() + w_at[f]);
+    for (size_t n = 0; n < fd.n; ++n) {
+      double ss = 0.0, cc = 0.0;
+      for (size_t k = 0; k < H; ++k) {
+        const float w = f16_bits_to_float(W[n * H + k]);
+        const f16 wg = (f16)(w * f16_bits_to_float(g[k]));
+        if (wf) wf[n * H + k] = wg;
+        ss += (double)(float)wg;
+        cc += (double)w * (double)f16_bits_to_float(be[k]);
+      }
+      fs[n] = (float)ss;
+      fc[n] = (float)(cc + (double)f16_bits_to_float(bias[n]));
+    }
+  }
+  void* dev = nullptr;
+  BBH_HIP(hipMalloc(&dev, cur), "hipMalloc(carried LayerNorm operands)");
+  const hipError_t e = hipMemcpy(dev, buf.data(), cur, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(dev);
+    return hip_fail(e, "hipMemcpy(carried LayerNorm operands)");
+  }
+  m->fold_blob = dev;
+  m->fold_bytes = cur;
+  const unsigned char* base = static_cast<const unsigned char*>(dev);
+  for (size_t f = 0; f < folds.size(); ++f) {
+    auto& l = m->layers[folds[f].layer];
+    const float* fs = reinterpret_cast<const float*>(base + vec_at[f]);
+    const f16* wf = ones[f] ? nullptr : reinterpret_cast<const f16*>(base + w_at[f]);
+    if (folds[f].qkv) {
+      l.qkv_fs = fs;
+      l.qkv_fc = fs + folds[f].n;
+      l.qkv_wf = wf ? wf : l.qkv_w;
+    } else {
+      l.f1_fs = fs;
+      l.f1_fc = fs + folds[f].n;
+      l.f1_wf = wf ? wf : l.f1_w;
+    }
+  }
+  return BBH_OK;
+}
+
 bbh_status model_from_host_blob(const std::vector<uint16_t>& host, bbh_model** out) {
   const BlobLayout& L = layout();
   bbh_model* m = new bbh_model();
@@ -207,6 +325,12 @@ bbh_status model_from_host_blob(const std::vector<uint16_t>& host, bbh_model** o
     l.f2_b = at(b0 + 13);
     l.ln2_g = at(b0 + 14);
     l.ln2_b = at(b0 + 15);
+  }
+  const bbh_status st = fold_operands(host, m);
+  if (st != BBH_OK) {
+    (void)hipFree(m->blob);
+    delete m;
+    return st;
   }
   *out = m;
   return BBH_OK;
@@ -324,16 +448,11 @@ bbh_status linear_residual_ln(OpTimer* t, hipStream_t s, int op, const f16* A, c
   });
 }
 
-bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
-                               const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
-                               OpTimer* t = nullptr, const Packed* pk = nullptr) {
+// Attention of the forward's sentences from ws->qkv into ws->ctx: packed
+// (pk) or per padded segment.
+bbh_status run_attention(bbh_workspace* ws, const Segment* segs, int n_segs, hipStream_t s,
+                         OpTimer* t, const Packed* pk) {
   const int H = BBH_HIDDEN;
-  BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H, ws->shared), 0, M, 3 * H, H,
-                          0.f}, [&] {
-    return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
-                                  bbh::Act::kNone, s, ws->shared),
-                        "qkv gemm");
-  }));
   if (pk) {
     BBH_TRY(timed_op(t, s, {BBH_OP_ATTENTION, -1, 0, pk->n, pk->max_len, BBH_NUM_HEADS, 0.f}, [&] {
       return check_launch(bbh::attention_packed(ws->qkv, ws->sents, pk->n, ws->ctx, BBH_NUM_HEADS,
@@ -349,6 +468,20 @@ bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, con
                           "attention");
     }));
   }
+  return BBH_OK;
+}
+
+bbh_status run_attention_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16* hidden,
+                               const Segment* segs, int n_segs, f16* out, int M, hipStream_t s,
+                               OpTimer* t = nullptr, const Packed* pk = nullptr) {
+  const int H = BBH_HIDDEN;
+  BBH_TRY(timed_op(t, s, {BBH_OP_QKV, bbh::gemm_tile(M, 3 * H, H, ws->shared), 0, M, 3 * H, H,
+                          0.f}, [&] {
+    return check_launch(bbh::gemm(hidden, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
+                                  bbh::Act::kNone, s, ws->shared),
+                        "qkv gemm");
+  }));
+  BBH_TRY(run_attention(ws, segs, n_segs, s, t, pk));
   return linear_residual_ln(t, s, BBH_OP_O_PROJ_LN, ws->ctx, L.o_w, L.o_b, hidden, L.ln1_g,
                             L.ln1_b, out, M, H, "o-proj gemm+ln", ws->shared);
 }
@@ -387,6 +520,104 @@ bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16
   return run_ffn_rows(ws, L, hidden, out, batch * seq, s, t);
 }
 
+// The six layers over M rows with their LayerNorms carried as row
+// statistics (bbh::LnCarry, M <= 8192): no LayerNorm pass between GEMMs.
+// `h0` holds the embedding LayerNorm's output.  Layer i's O-proj writes its
+// rows before ln1 to ws->attn_out (pairs in st_a); FFN1 normalises them on
+// the fly (writing their mean / rstd to mr_a), and FFN2 adds them, through
+// ln1, as its residual while writing the rows before ln2 (pairs in st_b),
+// which layer i + 1's QKV and O-proj read the same way (mr_b).  The last
+// layer writes final_out (which may be ws->attn_out: each residual chunk is
+// read by the thread that then overwrites it); its ln2 follows as a pass over
+// final_out, or is left to the caller (final_ln_deferred).  Timing records
+// of the carried GEMMs have fused_ln 2.
+bbh_status run_layers_carried(bbh_workspace* ws, const bbh_model* m, f16* h0, const Segment* segs,
+                              int n_segs, const Packed* pk, int M, f16* final_out, hipStream_t s,
+                              OpTimer* t, bool* final_ln_deferred) {
+  const int H = BBH_HIDDEN, F = BBH_FFN_DIM;
+  const float eps = BBH_LAYER_NORM_EPS;
+  const bool sh = ws->shared;
+  const f16* cur = h0;
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    const bbh_model::Layer& L = m->layers[i];
+    const bbh_model::Layer* P = i > 0 ? &m->layers[i - 1] : nullptr;  // its ln2 normalises cur
+    const bool last = i == BBH_NUM_LAYERS - 1;
+    f16* nxt = last ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
+    const int qkv_tile = bbh::gemm_tile(M, 3 * H, H, sh);
+    if (!P) {
+      BBH_TRY(timed_op(t, s, {BBH_OP_QKV, qkv_tile, 0, M, 3 * H, H, 0.f}, [&] {
+        return check_launch(bbh::gemm(cur, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
+                                      bbh::Act::kNone, s, sh),
+                            "qkv gemm");
+      }));
+    } else {
+      bbh::LnCarry cy;
+      cy.st_in = ws->st_b;
+      cy.mr_out = ws->mr_b;
+      cy.fs = L.qkv_fs;
+      cy.fc = L.qkv_fc;
+      BBH_TRY(timed_op(t, s, {BBH_OP_QKV, qkv_tile, 2, M, 3 * H, H, 0.f}, [&] {
+        return check_launch(bbh::gemm_fold(cur, L.qkv_wf, cy, ws->qkv, M, 3 * H, H,
+                                           bbh::Act::kNone, eps, s, sh),
+                            "qkv gemm (carried LayerNorm)");
+      }));
+    }
+    BBH_TRY(run_attention(ws, segs, n_segs, s, t, pk));
+    bool fused;
+    {
+      bbh::LnCarry cy;
+      cy.mr_in = P ? ws->mr_b : nullptr;
+      cy.st_out = ws->st_a;
+      BBH_TRY(timed_op(t, s, {BBH_OP_O_PROJ_LN, bbh::gemm_residual_ln_tile(M, H, &fused, sh), 2, M,
+                              H, H, 0.f}, [&] {
+        return check_launch(bbh::gemm_residual_stats(ws->ctx, L.o_w, L.o_b, cur,
+                                                     P ? P->ln2_g : nullptr,
+                                                     P ? P->ln2_b : nullptr, cy, ws->attn_out, M,
+                                                     H, s, sh),
+                            "o-proj gemm (row statistics)");
+      }));
+    }
+    {
+      bbh::LnCarry cy;
+      cy.st_in = ws->st_a;
+      cy.mr_out = ws->mr_a;
+      cy.fs = L.f1_fs;
+      cy.fc = L.f1_fc;
+      BBH_TRY(timed_op(t, s, {BBH_OP_FFN1_GELU, bbh::gemm_tile(M, F, H, sh), 2, M, F, H, 0.f}, [&] {
+        return check_launch(bbh::gemm_fold(ws->attn_out, L.f1_wf, cy, ws->inter, M, F, H,
+                                           bbh::Act::kGelu, eps, s, sh),
+                            "ffn1 gemm (carried LayerNorm)");
+      }));
+    }
+    {
+      bbh::LnCarry cy;
+      cy.mr_in = ws->mr_a;
+      cy.st_out = last ? nullptr : ws->st_b;
+      BBH_TRY(timed_op(t, s, {BBH_OP_FFN2_LN, bbh::gemm_residual_ln_tile(M, F, &fused, sh), 2, M, H,
+                              F, 0.f}, [&] {
+        return check_launch(bbh::gemm_residual_stats(ws->inter, L.f2_w, L.f2_b, ws->attn_out,
+                                                     L.ln1_g, L.ln1_b, cy, nxt, M, F, s, sh),
+                            "ffn2 gemm (row statistics)");
+      }));
+    }
+    cur = nxt;
+  }
+  if (final_ln_deferred) {
+    *final_ln_deferred = true;
+    return BBH_OK;
+  }
+  const bbh_model::Layer& L = m->layers[BBH_NUM_LAYERS - 1];
+  return timed_op(t, s, {BBH_OP_LAYERNORM, -1, 0, M, H, 0, 0.f}, [&] {
+    return check_launch(bbh::layernorm(final_out, nullptr, L.ln2_g, L.ln2_b, final_out, M, H, eps, s),
+                        "residual layernorm");
+  });
+}
+
+// Whether a forward of M rows carries its LayerNorms as row statistics.
+bool carries_ln(const bbh_workspace* ws, int M) {
+  return bbh::ln_carry_ok(M) && (size_t)M <= ws->carry_rows && ws->st_a;
+}
+
 // Embeddings + 6 layers over the segments' rows; the last layer writes
 // `final_out` (which may be ws->attn_out: the FFN2+LN epilogue reads each
 // residual element before the same thread overwrites it).  Segment g's
@@ -410,6 +641,9 @@ bbh_status run_encode_segs(bbh_workspace* ws, const bbh_model* m, const int32_t*
     }));
     M += sg.batch * sg.seq;
   }
+  if (carries_ln(ws, M))
+    return run_layers_carried(ws, m, ws->ping, segs, n_segs, nullptr, M, final_out, s, t,
+                              final_ln_deferred);
   f16* cur = ws->ping;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
@@ -432,6 +666,8 @@ bbh_status run_encode_packed(bbh_workspace* ws, const bbh_model* m, const int32_
                         "embedding+ln (packed)");
   }));
   if (M == 0) return BBH_OK;
+  if (carries_ln(ws, M))
+    return run_layers_carried(ws, m, ws->ping, nullptr, 0, &pk, M, final_out, s, t, nullptr);
   f16* cur = ws->ping;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     f16* nxt = (i == BBH_NUM_LAYERS - 1) ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
@@ -775,19 +1011,21 @@ bbh_status bbh_model_load_safetensors(const char* path, bbh_model** out) {
 bbh_status bbh_model_free(bbh_model* m) {
   if (!m) return BBH_OK;
   hipError_t e = m->blob ? hipFree(m->blob) : hipSuccess;
+  const hipError_t e2 = m->fold_blob ? hipFree(m->fold_blob) : hipSuccess;
+  if (e == hipSuccess) e = e2;
   delete m;
   if (e != hipSuccess) return hip_fail(e, "hipFree(weights)");
   return BBH_OK;
 }
 
-size_t bbh_model_device_bytes(const bbh_model* m) { return m ? m->bytes : 0; }
+size_t bbh_model_device_bytes(const bbh_model* m) { return m ? m->bytes + m->fold_bytes : 0; }
 
 size_t bbh_workspace_bytes(int max_batch, int max_seq) {
   if (max_batch < 1 || max_seq < 1) return 0;
   const size_t rows = (size_t)max_batch * max_seq;
   const size_t H = BBH_HIDDEN;
   return align256(rows * 3 * H * 2) + align256(rows * BBH_FFN_DIM * 2) + 4 * align256(rows * H * 2) +
-         align256(rows * sizeof(bbh::PackedSentence));
+         align256(rows * sizeof(bbh::PackedSentence)) + carry_bytes(rows);
 }
 
 bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out) {
@@ -825,6 +1063,11 @@ bbh_status bbh_workspace_create(int max_batch, int max_seq, bbh_workspace** out)
   ws->ping = take(rows * H * 2);
   ws->pong = take(rows * H * 2);
   ws->sents = reinterpret_cast<bbh::PackedSentence*>(take(rows * sizeof(bbh::PackedSentence)));
+  ws->carry_rows = carry_rows(rows);
+  ws->st_a = reinterpret_cast<float2*>(take(ws->carry_rows * bbh::kMaxCarryTiles * sizeof(float2)));
+  ws->st_b = reinterpret_cast<float2*>(take(ws->carry_rows * bbh::kMaxCarryTiles * sizeof(float2)));
+  ws->mr_a = reinterpret_cast<float2*>(take(ws->carry_rows * sizeof(float2)));
+  ws->mr_b = reinterpret_cast<float2*>(take(ws->carry_rows * sizeof(float2)));
   *out = ws;
   return BBH_OK;
 }
@@ -855,14 +1098,15 @@ bbh_status bbh_embed(bbh_workspace* ws, const bbh_model* m, const int32_t* ids,
 // ---- bbh_embed without a workspace ------------------------------------------
 // The forward's activations in a file-scope device array instead of a
 // workspace: BBH_NOALLOC_MAX_ROWS rows of the same six buffers (8,448 bytes a
-// row; 69.2 MB), which every GPU the library runs on holds until the process
-// ends.  Host code never names the array in a kernel argument or copy: its
+// row) and the carried-LayerNorm statistics (112 bytes a row); 70.1 MB, which
+// every GPU the library runs on holds until the process ends.  Host code never names the array in a kernel argument or copy: its
 // address on each device comes from hipGetSymbolAddress, taken once per
 // device with that device current (the entry point's first call there).
 namespace {
 constexpr size_t kScratchRowBytes =
     (3 * (size_t)BBH_HIDDEN + BBH_FFN_DIM + 4 * (size_t)BBH_HIDDEN) * sizeof(f16);
-constexpr size_t kScratchBytes = (size_t)BBH_NOALLOC_MAX_ROWS * kScratchRowBytes;
+constexpr size_t kScratchBytes =
+    (size_t)BBH_NOALLOC_MAX_ROWS * kScratchRowBytes + carry_bytes(BBH_NOALLOC_MAX_ROWS);
 static_assert(BBH_NOALLOC_MAX_ROWS % 64 == 0, "each buffer stays 256-byte aligned");
 constexpr int kMaxDevices = 64;
 
@@ -919,6 +1163,17 @@ bbh_status bbh_embed_noalloc(const bbh_model* m, const int32_t* ids, const int32
   ws.ping = ws.attn_out + R * H;
   ws.pong = ws.ping + R * H;
   ws.sents = nullptr;  // padded forwards only
+  ws.carry_rows = carry_rows(R);
+  unsigned char* c = reinterpret_cast<unsigned char*>(ws.pong + R * H);
+  auto take = [&](size_t bytes) {
+    float2* r = reinterpret_cast<float2*>(c);
+    c += align256(bytes);
+    return r;
+  };
+  ws.st_a = take(ws.carry_rows * bbh::kMaxCarryTiles * sizeof(float2));
+  ws.st_b = take(ws.carry_rows * bbh::kMaxCarryTiles * sizeof(float2));
+  ws.mr_a = take(ws.carry_rows * sizeof(float2));
+  ws.mr_b = take(ws.carry_rows * sizeof(float2));
   const hipStream_t s = S(stream);
   bool ln_deferred = false;  // no caller sees these rows
   BBH_TRY(run_encode(&ws, m, ids, types, mask, ws.attn_out, batch, seq, s, nullptr, &ln_deferred));

@@ -40,7 +40,8 @@
 namespace bbh {
 namespace {
 
-enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3 };
+// kFold / kFoldGelu and kResStats: the two sides of LnCarry (kernels.h).
+enum Epi { kBias = 0, kGelu = 1, kResidual = 2, kLayerNorm = 3, kFold = 4, kFoldGelu = 5, kResStats = 6 };
 
 template <int BM_, int BN_, int WM_, int WN_, int SA_, int PD_ = 0, int SW_ = 2>
 struct Cfg {
@@ -379,14 +380,21 @@ struct ResidualAhead {
   static constexpr int CPR = C::BN / 8;
   static constexpr int PER = (C::BM * CPR + C::THREADS - 1) / C::THREADS;
   static constexpr bool kOn = C::NPASS == 1 && PER <= 4;
+  // (mean, rstd) of the chunk's row, with a carried LayerNorm, for tiles with
+  // at most two chunks a thread (the others load it when they store).
+  static constexpr bool kMr = kOn && PER <= 2;
   f16x8 r[kOn ? PER : 1];
-  __device__ __forceinline__ void load(const f16* residual, int ldc, int M, int m0, int n0) {
+  float2 mr[kMr ? PER : 1];
+  __device__ __forceinline__ void load(const f16* residual, int ldc, int M, int m0, int n0,
+                                       const float2* mr_in = nullptr) {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int idx = threadIdx.x + q * C::THREADS;
       const int row = idx / CPR, c = idx % CPR;
-      if (idx < C::BM * CPR && m0 + row < M)
+      if (idx < C::BM * CPR && m0 + row < M) {
         r[q] = *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + row) * ldc + n0 + c * 8);
+        if (kMr && mr_in) mr[q] = mr_in[m0 + row];
+      }
     }
   }
 };
@@ -418,11 +426,118 @@ __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ ou
   }
 }
 
+// store_rows for kResStats: the residual, brought through its LayerNorm when
+// cy.mr_in is given, is added in fp32 to the fp16 tile value; then the mean
+// and the sum of squared deviations of each stored fp16 row over each
+// 64-column group go to cy.st_out (pair n / 64 of the row), summed in the
+// same order whatever the tile width, so the statistics, and all that is
+// computed from them, do not depend on the tile.  A row's CPR = BN / 8
+// threads are consecutive lanes of one wavefront, so every lane of such a
+// group takes the same branches.
+template <class C, int ROWS>
+__device__ __forceinline__ void store_rows_stats(const f16* tile, f16* __restrict__ out, int M,
+                                                 int m0, int n0, const f16* residual,
+                                                 const f16* __restrict__ gamma,
+                                                 const f16* __restrict__ beta, const LnCarry& cy,
+                                                 const ResidualAhead<C>* ahead) {
+  constexpr int CPR = C::BN / 8, N = kHidden;
+  static_assert(CPR == 8 || CPR == 16, "a row's chunks on 8 or 16 lanes");
+  constexpr int PER = (ROWS * CPR + C::THREADS - 1) / C::THREADS;
+  constexpr int kUnroll = C::NPASS == 1 ? PER : 4;
+  static_assert(C::THREADS % CPR == 0, "a thread keeps its chunk column");
+  // A thread's chunks all sit in chunk column threadIdx.x % CPR: gamma and
+  // beta of its 8 columns once.
+  const int c = threadIdx.x % CPR;
+  f16x8 g = {}, b = {};
+  // (mean, rstd) of the thread's chunk rows: loaded with the residual before
+  // the K loop (ResidualAhead::kMr, ahead given then), else all issued
+  // together here (rows clamped into the matrix).
+  constexpr bool kMrAhead = ResidualAhead<C>::kMr;
+  float2 mrs[kMrAhead ? 1 : PER];
+  if (cy.mr_in) {
+    g = *reinterpret_cast<const f16x8*>(gamma + n0 + c * 8);
+    b = *reinterpret_cast<const f16x8*>(beta + n0 + c * 8);
+    if constexpr (!kMrAhead) {
+#pragma unroll
+      for (int q = 0; q < PER; ++q)
+        mrs[q] = cy.mr_in[min(m0 + (int)(threadIdx.x + q * C::THREADS) / CPR, M - 1)];
+    }
+  }
+#pragma unroll kUnroll
+  for (int q = 0; q < PER; ++q) {
+    const int idx = threadIdx.x + q * C::THREADS;
+    const int r = idx / CPR;
+    if (idx < ROWS * CPR && m0 + r < M) {
+      const f16x8 v = *reinterpret_cast<const f16x8*>(tile + r * C::OUT_LD + c * 8);
+      const size_t at = (size_t)(m0 + r) * N + n0 + c * 8;
+      const f16x8 rv = ahead ? ahead->r[q] : *reinterpret_cast<const f16x8*>(residual + at);
+      float y[8];
+      if (cy.mr_in) {
+        float2 mr;
+        if constexpr (kMrAhead)
+          mr = ahead->mr[q];
+        else
+          mr = mrs[q];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          y[i] = (float)v[i] + (((float)rv[i] - mr.x) * mr.y * (float)g[i] + (float)b[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = (float)v[i] + (float)rv[i];
+      }
+      f16x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        o[i] = (f16)y[i];
+        y[i] = (float)o[i];  // the statistics describe the stored fp16 row
+      }
+      *reinterpret_cast<f16x8*>(out + at) = o;
+      if (cy.st_out) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t += y[i];
+        t = xor_op<1>(t, AddOp{});
+        t = xor_op<2>(t, AddOp{});
+        t = xor_op<4>(t, AddOp{});
+        const float mean = t * (1.0f / 64);
+        float d2 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d2 += (y[i] - mean) * (y[i] - mean);
+        d2 = xor_op<1>(d2, AddOp{});
+        d2 = xor_op<2>(d2, AddOp{});
+        d2 = xor_op<4>(d2, AddOp{});
+        if ((c & 7) == 0)
+          cy.st_out[(size_t)(m0 + r) * kMaxCarryTiles + (n0 + c * 8) / 64] = make_float2(mean, d2);
+      }
+    }
+  }
+}
+
+// (mean, rstd) of a 384-wide row from the (mean, sum of squared deviations)
+// pairs of its six 64-column groups (the pairwise update of Chan, Golub and
+// LeVeque over all groups at once): the population variance the LayerNorm
+// pass takes.
+__device__ __forceinline__ float2 carried_row_stats(const float2 (&p)[kMaxCarryTiles], float eps) {
+  float t = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxCarryTiles; ++k) t += p[k].x;
+  const float mean = t * (1.0f / kMaxCarryTiles);
+  float m2 = 0.f, d2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxCarryTiles; ++k) {
+    const float d = p[k].x - mean;
+    m2 += p[k].y;
+    d2 += d * d;
+  }
+  m2 += d2 * 64.f;
+  return make_float2(mean, rsqrtf(m2 * (1.0f / kHidden) + eps));
+}
+
 template <class C, int EPI>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
     const f16* __restrict__ A, const f16* __restrict__ W, const f16* __restrict__ bias,
     const f16* residual, const f16* __restrict__ gamma, const f16* __restrict__ beta, f16* out,
-    int M, int N, int K, float eps) {
+    int M, int N, int K, float eps, LnCarry cy) {
   HIP_DYNAMIC_SHARED(f16, smem);
   int mi, ni;
   if (!tile_of(N / C::BN, (M + C::BM - 1) / C::BM, mi, ni)) return;
@@ -438,15 +553,24 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   // Tiles with one or two 32-column blocks per wavefront and no LayerNorm
   // (8-16 VGPRs) load them before the K loop, as they do the residual, so
   // the loads' latency hides behind it.
-  constexpr bool kHoist = C::FM * C::FN <= 8;
+  // The carried-LayerNorm GEMMs (kFold*) take fp32 fs / fc per column in
+  // place of the bias, once per column block.
+  constexpr bool kFoldE = EPI == kFold || EPI == kFoldGelu;
+  constexpr bool kHoist = C::FM * C::FN <= 8 && !kFoldE;
   constexpr bool kColsAhead = kHoist && EPI != kLayerNorm && C::FN <= 2;
   constexpr int HN = kHoist ? C::FN : 1;
   f16x4 bvs[HN][4], gvs[EPI == kLayerNorm ? HN : 1][4], evs[EPI == kLayerNorm ? HN : 1][4];
+  f32x4 fsv[kFoldE ? 4 : 1], fcv[kFoldE ? 4 : 1];
   auto load_cols = [&](int fn, int h) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
-      bvs[h][j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
+      if constexpr (kFoldE) {
+        fsv[j] = *reinterpret_cast<const f32x4*>(cy.fs + n0 + nl);
+        fcv[j] = *reinterpret_cast<const f32x4*>(cy.fc + n0 + nl);
+      } else {
+        bvs[h][j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
+      }
       if constexpr (EPI == kLayerNorm) {
         gvs[h][j] = *reinterpret_cast<const f16x4*>(gamma + nl);
         evs[h][j] = *reinterpret_cast<const f16x4*>(beta + nl);
@@ -457,9 +581,25 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 #pragma unroll
     for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
   }
-  constexpr bool kAhead = EPI == kResidual && ResidualAhead<C>::kOn;
+  constexpr bool kAhead = (EPI == kResidual || EPI == kResStats) && ResidualAhead<C>::kOn;
   ResidualAhead<C> ahead;
-  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0);
+  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0, EPI == kResStats ? cy.mr_in : nullptr);
+  // kFold*: thread t < BM loads the six group pairs of tile row t (48
+  // bytes) before the K loop, so that their latency hides behind it.
+  float2 rp[kFoldE ? kMaxCarryTiles : 1];
+  if constexpr (kFoldE) {
+    static_assert(C::THREADS >= C::BM, "a thread per tile row");
+    if (threadIdx.x < C::BM) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(
+          cy.st_in + (size_t)min(m0 + (int)threadIdx.x, M - 1) * kMaxCarryTiles);
+#pragma unroll
+      for (int k = 0; k < kMaxCarryTiles / 2; ++k) {
+        const f32x4 v = src[k];
+        rp[2 * k] = make_float2(v[0], v[1]);
+        rp[2 * k + 1] = make_float2(v[2], v[3]);
+      }
+    }
+  }
   f32x16 acc[C::FM][C::FN];
   if constexpr (C::PD > 0)
     mainloop_reg<C>(A, W, M, K, m0, n0, smem, acc);
@@ -475,6 +615,24 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   if constexpr (kHoist && !kColsAhead) {
 #pragma unroll
     for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
+  }
+  if constexpr (kFoldE) {
+    // Each row's (mean, rstd) once, by its loader thread, into the LayerNorm
+    // partials area (free for these epilogues), then to every lane of the row.
+    if (threadIdx.x < C::BM) {
+      const float2 st = carried_row_stats(rp, eps);
+      red[2 * threadIdx.x] = st.x;
+      red[2 * threadIdx.x + 1] = st.y;
+      const int m = m0 + (int)threadIdx.x;
+      if (ni == 0 && m < M && cy.mr_out) cy.mr_out[m] = st;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int fm = 0; fm < C::FM; ++fm) {
+      const int row = wm * C::TM + fm * 32 + r32;
+      mean[fm] = red[2 * row];
+      rstd[fm] = red[2 * row + 1];
+    }
   }
 
   if constexpr (EPI == kLayerNorm) {
@@ -590,6 +748,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
                 o[i] = to_half((acc[fm][fn][4 * j + i] - mean[fm]) * rstd[fm] *
                                    (float)gvs[h][j][i] +
                                (float)evs[h][j][i]);
+            } else if constexpr (kFoldE) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float v = fmaf(-mean[fm], fsv[j][i], acc[fm][fn][4 * j + i]) * rstd[fm] + fcv[j][i];
+                if (EPI == kFoldGelu) v = gelu_poly(v);
+                o[i] = to_half(v);
+              }
             } else {
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
@@ -605,8 +770,12 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       }
     }
     lds_barrier();
-    store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr,
-                      kAhead ? ahead.r : nullptr);
+    if constexpr (EPI == kResStats)
+      store_rows_stats<C, PR>(tile, out, M, m0 + p * PR, n0, residual, gamma, beta, cy,
+                              kAhead ? &ahead : nullptr);
+    else
+      store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr,
+                        kAhead ? ahead.r : nullptr);
     if (p + 1 < C::NPASS) lds_barrier();
   }
 }
@@ -945,9 +1114,11 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
 template <class C, int EPI>
 hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residual,
                   const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
-                  hipStream_t s) {
+                  hipStream_t s, const LnCarry& cy = LnCarry{}) {
   if constexpr (EPI == kLayerNorm && C::BN != kHidden) {
     return hipErrorInvalidValue;  // LayerNorm needs a tile that owns whole rows
+  } else if constexpr (EPI == kResStats && C::BN != 64 && C::BN != 128) {
+    return hipErrorInvalidValue;  // row statistics over 8 or 16 lanes
   } else {
     if (N % C::BN != 0) return hipErrorInvalidValue;
     static const hipError_t attr = hipFuncSetAttribute(
@@ -962,9 +1133,14 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
       const int mr = std::min(step, M - r0);
       const int nb = N / C::BN, mb = (mr + C::BM - 1) / C::BM;
       const int grid = nb * 8 * ((mb + 7) / 8);
+      LnCarry cr = cy;  // row-indexed like A and out
+      if (cr.st_in) cr.st_in += (size_t)r0 * kMaxCarryTiles;
+      if (cr.mr_out) cr.mr_out += r0;
+      if (cr.mr_in) cr.mr_in += r0;
+      if (cr.st_out) cr.st_out += (size_t)r0 * kMaxCarryTiles;
       hipLaunchKernelGGL((gemm_kernel<C, EPI>), dim3(grid), dim3(C::THREADS), C::LDS, s,
                          A + (size_t)r0 * K, W, bias, residual ? residual + (size_t)r0 * N : nullptr,
-                         gamma, beta, out + (size_t)r0 * N, mr, N, K, eps);
+                         gamma, beta, out + (size_t)r0 * N, mr, N, K, eps, cr);
       const hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
@@ -1037,6 +1213,19 @@ hipError_t launch(const f16* A, const f16* W, const f16* bias, const f16* residu
 #endif
 
 constexpr int kTiles = 33;  // kTiles names the weight-resident kernel (no tile has this id)
+
+// The Cfg of a product tile id.
+template <int ID>
+struct TileOf;
+#define BBH_TILE_TYPE(ID, BM, BN, WM, WN, SA, PD, SW) \
+  template <>                                         \
+  struct TileOf<ID> {                                 \
+    using type = Cfg<BM, BN, WM, WN, SA, PD, SW>;     \
+  };
+BBH_TILES(BBH_TILE_TYPE)
+#undef BBH_TILE_TYPE
+template <int ID>
+using TileCfg = typename TileOf<ID>::type;
 
 template <int EPI>
 hipError_t launch_id(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
@@ -1185,6 +1374,53 @@ hipError_t gemm_residual_ln(const f16* A, const f16* W, const f16* bias, const f
   hipError_t e = gemm_residual(A, W, bias, residual, y, M, K, s, shared);
   if (e != hipSuccess) return e;
   return layernorm(y, nullptr, gamma, beta, y, M, kHidden, eps, s);
+}
+
+// The carried-LayerNorm epilogues are built for the tiles pick_plain chooses
+// up to 8192 rows.
+template <int EPI>
+hipError_t launch_carry(int id, const f16* A, const f16* W, const f16* bias, const f16* residual,
+                        const f16* gamma, const f16* beta, f16* out, int M, int N, int K, float eps,
+                        hipStream_t s, const LnCarry& cy) {
+#define BBH_CARRY(ID)                                                                          \
+  case ID:                                                                                     \
+    return launch<TileCfg<ID>, EPI>(A, W, bias, residual, gamma, beta, out, M, N, K, eps, s, cy);
+  switch (id) {
+    BBH_CARRY(0)
+    BBH_CARRY(1)
+    BBH_CARRY(26)
+    BBH_CARRY(30)
+    BBH_CARRY(31)
+    BBH_CARRY(32)
+    BBH_CARRY(34)
+  }
+#undef BBH_CARRY
+  return hipErrorInvalidValue;
+}
+
+bool ln_carry_ok(int M) { return M >= 1 && M <= 8192; }
+
+hipError_t gemm_fold(const f16* A, const f16* W, const LnCarry& cy, f16* C, int M, int N, int K,
+                     Act act, float eps, hipStream_t s, bool shared) {
+  const bool aligned = (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C) & 15) == 0 &&
+                       (((uintptr_t)cy.fs | (uintptr_t)cy.fc) & 15) == 0;
+  if (!ln_carry_ok(M) || !gemm_mfma_ok(N, K) || !aligned || !cy.st_in || !cy.fs || !cy.fc ||
+      wres_ok(M, N, K))
+    return hipErrorInvalidValue;
+  const int id = pick_plain(M, N, K, shared);
+  return act == Act::kGelu
+             ? launch_carry<kFoldGelu>(id, A, W, nullptr, nullptr, nullptr, nullptr, C, M, N, K, eps, s, cy)
+             : launch_carry<kFold>(id, A, W, nullptr, nullptr, nullptr, nullptr, C, M, N, K, eps, s, cy);
+}
+
+hipError_t gemm_residual_stats(const f16* A, const f16* W, const f16* bias, const f16* residual,
+                               const f16* gamma, const f16* beta, const LnCarry& cy, f16* y,
+                               int M, int K, hipStream_t s, bool shared) {
+  bool fused;
+  const int id = gemm_residual_ln_tile(M, K, &fused, shared);
+  if (fused || !ln_carry_ok(M) || (cy.mr_in && (!gamma || !beta))) return hipErrorInvalidValue;
+  return launch_carry<kResStats>(id, A, W, bias, residual, gamma, beta, y, M, kHidden, K, 0.f, s,
+                                 cy);
 }
 
 hipError_t gemm_residual(const f16* A, const f16* W, const f16* bias, const f16* residual, f16* y,

@@ -28,6 +28,35 @@ bool gemm_mfma_ok(int N, int K);
 hipError_t gemm(const f16* A, const f16* W, const f16* bias, f16* C, int M, int N,
                 int K, Act act, hipStream_t s, bool shared = false);
 
+// The encoder's LayerNorms carried between its GEMMs as row statistics
+// instead of passes of their own, where the residual GEMM tiles do not own
+// whole rows (M <= 8192, ln_carry_ok).  A residual GEMM (gemm_residual_stats)
+// writes y = A . W^T + bias + R un-normalised, and for each row the mean and
+// the sum of squared deviations of its fp16 outputs over each of its six
+// 64-column groups (st_out: kMaxCarryTiles pairs a row, the same bits
+// whatever the tile).  R is the residual as given, or, with
+// mr_in, the residual rows brought through their LayerNorm on the fly from
+// each row's (mean, rstd).  The GEMM that reads y (gemm_fold: QKV, FFN1)
+// combines a row's pairs into its mean and rstd, writes those (mr_out, by the
+// workgroups of the first column tile) for the next residual GEMM, and gives
+// LN(y) . W^T + bias as rstd * (y . W'^T - mean * fs) + fc, W' = W diag(gamma)
+// in fp16, fs = row sums of W', fc = W . beta + bias (fp32, per column).
+struct LnCarry {
+  const float2* st_in = nullptr;  // gemm_fold: the input rows' group pairs
+  float2* mr_out = nullptr;       // gemm_fold: (mean, rstd) per row
+  const float* fs = nullptr;      // gemm_fold: per output column
+  const float* fc = nullptr;
+  const float2* mr_in = nullptr;  // gemm_residual_stats: (mean, rstd) of the residual rows
+  float2* st_out = nullptr;       // gemm_residual_stats: the output rows' group pairs
+};
+constexpr int kMaxCarryTiles = 6;  // 64-column groups of a 384-wide row
+bool ln_carry_ok(int M);
+hipError_t gemm_fold(const f16* A, const f16* W, const LnCarry& cy, f16* C, int M, int N, int K,
+                     Act act, float eps, hipStream_t s, bool shared = false);
+hipError_t gemm_residual_stats(const f16* A, const f16* W, const f16* bias, const f16* residual,
+                               const f16* gamma, const f16* beta, const LnCarry& cy, f16* y,
+                               int M, int K, hipStream_t s, bool shared = false);
+
 // Tile configuration gemm() / gemm_residual_ln() launch for a shape (-1: the
 // plain tiled kernel), whether the LayerNorm is inside the GEMM kernel, and
 // the configuration's name as it appears in the kernel symbol.

@@ -64,10 +64,14 @@ def test_status_strings():
 def test_workspace_bytes():
     L = _lib()
     rows = 64 * 128
-    # QKV, FFN intermediate, four (rows, 384) buffers, and the packed-forward
-    # sentence table (24 bytes per possible sentence)
+    # QKV, FFN intermediate, four (rows, 384) buffers, the packed-forward
+    # sentence table (24 bytes per possible sentence), and the carried
+    # LayerNorm statistics of up to 8192 rows (two buffers of 6 float pairs
+    # a row, two of one pair a row)
+    rc = min(rows, 8192)
     want = sum((n + 255) // 256 * 256
-               for n in [rows * 1152 * 2, rows * 1536 * 2] + [rows * 384 * 2] * 4 + [rows * 24])
+               for n in [rows * 1152 * 2, rows * 1536 * 2] + [rows * 384 * 2] * 4 + [rows * 24]
+               + [rc * 48] * 2 + [rc * 8] * 2)
     assert L.bbh_workspace_bytes(64, 128) == want
     assert L.bbh_workspace_bytes(0, 128) == 0
 

@@ -129,7 +129,7 @@ bbh_status bbh_embed(bbh_workspace *ws, const bbh_model *m, const int32_t *ids,
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments and results as bbh_embed
  * without the workspace: the forward's activations live in a device array of
- * the library (BBH_NOALLOC_MAX_ROWS rows, 69.2 MB on each GPU it runs on,
+ * the library (BBH_NOALLOC_MAX_ROWS rows, 70.1 MB on each GPU it runs on,
  * held until the process ends), so the call performs no allocation of any
  * kind on the success path.  batch*seq above BBH_NOALLOC_MAX_ROWS fails with
  * BBH_ERR_CAPACITY before anything is enqueued.  Every call on one GPU uses
@@ -290,14 +290,18 @@ typedef enum bbh_op {
   BBH_OP_FFN2_LN = 5,   /* output Linear + residual (+ LayerNorm when fused) */
   BBH_OP_EMBED = 6,     /* embedding gather + embedding LayerNorm */
   BBH_OP_POOL = 7,      /* masked mean pool + L2 normalize */
-  BBH_OP_LAYERNORM = 8, /* residual LayerNorm pass after an unfused O-proj / FFN2 */
+  BBH_OP_LAYERNORM = 8, /* residual LayerNorm pass after an unfused O-proj / FFN2, or the last
+                           layer's when the LayerNorms are carried */
   BBH_OP_FFN = 9        /* the whole FFN block (intermediate Linear + GELU, output Linear +
                            residual + LayerNorm) in one kernel, at large M */
 } bbh_op;
 typedef struct bbh_launch_time {
   int op;       /* bbh_op */
   int tile;     /* GEMM tile configuration (bbh_gemm_tile_name); -1 for other ops */
-  int fused_ln; /* O-proj / FFN2: 1 when the LayerNorm runs inside the GEMM kernel, 0 when it
+  int fused_ln; /* 2: the LayerNorm carried as row statistics (forwards of at most 8192 rows):
+                   O-proj / FFN2 write the rows before it with their statistics and no pass
+                   follows; QKV (from layer 1) / FFN1 normalise their input rows from them.
+                   O-proj / FFN2: 1 when the LayerNorm runs inside the GEMM kernel, 0 when it
                    follows as its own BBH_OP_LAYERNORM record */
   int m, n, k;  /* GEMM (M, N, K); attention (batch, seq, heads); embed / pool / LayerNorm
                    (rows or sentences, seq or 384, 0); FFN (M, 384, 1536) */

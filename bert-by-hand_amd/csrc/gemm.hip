@@ -380,20 +380,14 @@ struct ResidualAhead {
   static constexpr int CPR = C::BN / 8;
   static constexpr int PER = (C::BM * CPR + C::THREADS - 1) / C::THREADS;
   static constexpr bool kOn = C::NPASS == 1 && PER <= 4;
-  // (mean, rstd) of the chunk's row, with a carried LayerNorm, for tiles with
-  // at most two chunks a thread (the others load it when they store).
-  static constexpr bool kMr = kOn && PER <= 2;
   f16x8 r[kOn ? PER : 1];
-  float2 mr[kMr ? PER : 1];
-  __device__ __forceinline__ void load(const f16* residual, int ldc, int M, int m0, int n0,
-                                       const float2* mr_in = nullptr) {
+  __device__ __forceinline__ void load(const f16* residual, int ldc, int M, int m0, int n0) {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int idx = threadIdx.x + q * C::THREADS;
       const int row = idx / CPR, c = idx % CPR;
       if (idx < C::BM * CPR && m0 + row < M) {
         r[q] = *reinterpret_cast<const f16x8*>(residual + (size_t)(m0 + row) * ldc + n0 + c * 8);
-        if (kMr && mr_in) mr[q] = mr_in[m0 + row];
       }
     }
   }
@@ -427,7 +421,9 @@ __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ ou
 }
 
 // store_rows for kResStats: the residual, brought through its LayerNorm when
-// cy.mr_in is given, is added in fp32 to the fp16 tile value; then the mean
+// cy.mr_in is given (the rows' (mean, rstd) and the columns' gamma / beta
+// staged in LDS: rmr for the pass's rows, rgb), is added in fp32 to the fp16
+// tile value; then the mean
 // and the sum of squared deviations of each stored fp16 row over each
 // 64-column group go to cy.st_out (pair n / 64 of the row), summed in the
 // same order whatever the tile width, so the statistics, and all that is
@@ -437,8 +433,8 @@ __device__ __forceinline__ void store_rows(const f16* tile, f16* __restrict__ ou
 template <class C, int ROWS>
 __device__ __forceinline__ void store_rows_stats(const f16* tile, f16* __restrict__ out, int M,
                                                  int m0, int n0, const f16* residual,
-                                                 const f16* __restrict__ gamma,
-                                                 const f16* __restrict__ beta, const LnCarry& cy,
+                                                 const float2* rmr, const f16* rgb,
+                                                 const LnCarry& cy,
                                                  const ResidualAhead<C>* ahead) {
   constexpr int CPR = C::BN / 8, N = kHidden;
   static_assert(CPR == 8 || CPR == 16, "a row's chunks on 8 or 16 lanes");
@@ -449,19 +445,9 @@ __device__ __forceinline__ void store_rows_stats(const f16* tile, f16* __restric
   // beta of its 8 columns once.
   const int c = threadIdx.x % CPR;
   f16x8 g = {}, b = {};
-  // (mean, rstd) of the thread's chunk rows: loaded with the residual before
-  // the K loop (ResidualAhead::kMr, ahead given then), else all issued
-  // together here (rows clamped into the matrix).
-  constexpr bool kMrAhead = ResidualAhead<C>::kMr;
-  float2 mrs[kMrAhead ? 1 : PER];
   if (cy.mr_in) {
-    g = *reinterpret_cast<const f16x8*>(gamma + n0 + c * 8);
-    b = *reinterpret_cast<const f16x8*>(beta + n0 + c * 8);
-    if constexpr (!kMrAhead) {
-#pragma unroll
-      for (int q = 0; q < PER; ++q)
-        mrs[q] = cy.mr_in[min(m0 + (int)(threadIdx.x + q * C::THREADS) / CPR, M - 1)];
-    }
+    g = *reinterpret_cast<const f16x8*>(rgb + c * 8);
+    b = *reinterpret_cast<const f16x8*>(rgb + C::BN + c * 8);
   }
 #pragma unroll kUnroll
   for (int q = 0; q < PER; ++q) {
@@ -473,11 +459,7 @@ __device__ __forceinline__ void store_rows_stats(const f16* tile, f16* __restric
       const f16x8 rv = ahead ? ahead->r[q] : *reinterpret_cast<const f16x8*>(residual + at);
       float y[8];
       if (cy.mr_in) {
-        float2 mr;
-        if constexpr (kMrAhead)
-          mr = ahead->mr[q];
-        else
-          mr = mrs[q];
+        const float2 mr = rmr[r];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           y[i] = (float)v[i] + (((float)rv[i] - mr.x) * mr.y * (float)g[i] + (float)b[i]);
@@ -561,13 +543,16 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   constexpr int HN = kHoist ? C::FN : 1;
   f16x4 bvs[HN][4], gvs[EPI == kLayerNorm ? HN : 1][4], evs[EPI == kLayerNorm ? HN : 1][4];
   f32x4 fsv[kFoldE ? 4 : 1], fcv[kFoldE ? 4 : 1];
+  // kFold*: fs / fc of the tile's columns in LDS after the row statistics
+  // (written after the K loop; `fcol` is set there).
+  const float* fcol = nullptr;
   auto load_cols = [&](int fn, int h) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int nl = wn * C::TN + fn * 32 + 8 * j + 4 * kh;
       if constexpr (kFoldE) {
-        fsv[j] = *reinterpret_cast<const f32x4*>(cy.fs + n0 + nl);
-        fcv[j] = *reinterpret_cast<const f32x4*>(cy.fc + n0 + nl);
+        fsv[j] = *reinterpret_cast<const f32x4*>(fcol + nl);
+        fcv[j] = *reinterpret_cast<const f32x4*>(fcol + C::BN + nl);
       } else {
         bvs[h][j] = bias ? *reinterpret_cast<const f16x4*>(bias + n0 + nl) : f16x4{0, 0, 0, 0};
       }
@@ -583,12 +568,39 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   }
   constexpr bool kAhead = (EPI == kResidual || EPI == kResStats) && ResidualAhead<C>::kOn;
   ResidualAhead<C> ahead;
-  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0, EPI == kResStats ? cy.mr_in : nullptr);
+  if constexpr (kAhead) ahead.load(residual, N, M, m0, n0);
+  // kResStats with a carried residual: thread t < BM loads tile row t's
+  // (mean, rstd), thread t < BN gamma / beta of tile column t; they go
+  // through LDS to the store threads.  Before the K loop where the tile
+  // keeps at most two residual chunks a thread in registers, after it
+  // otherwise (the registers would cost the larger tiles occupancy).
+  float2 smr = make_float2(0.f, 0.f);
+  f16 sg = 0, sb = 0;
+  auto load_carry = [&] {
+    if (cy.mr_in) {
+      if (threadIdx.x < C::BM) smr = cy.mr_in[min(m0 + (int)threadIdx.x, M - 1)];
+      if (threadIdx.x < C::BN) {
+        sg = gamma[n0 + threadIdx.x];
+        sb = beta[n0 + threadIdx.x];
+      }
+    }
+  };
+  constexpr bool kCarryAhead = ResidualAhead<C>::PER <= 2;
+  if constexpr (EPI == kResStats) {
+    static_assert(C::THREADS >= C::BM && C::THREADS >= C::BN, "a thread per tile row / column");
+    if constexpr (kCarryAhead) load_carry();
+  }
   // kFold*: thread t < BM loads the six group pairs of tile row t (48
-  // bytes) before the K loop, so that their latency hides behind it.
+  // bytes), and thread t < BN fs / fc of tile column t, before the K loop,
+  // so that their latency hides behind it.
   float2 rp[kFoldE ? kMaxCarryTiles : 1];
+  float cs = 0.f, cc = 0.f;
   if constexpr (kFoldE) {
-    static_assert(C::THREADS >= C::BM, "a thread per tile row");
+    static_assert(C::THREADS >= C::BM && C::THREADS >= C::BN, "a thread per tile row / column");
+    if (threadIdx.x < C::BN) {
+      cs = cy.fs[n0 + threadIdx.x];
+      cc = cy.fc[n0 + threadIdx.x];
+    }
     if (threadIdx.x < C::BM) {
       const f32x4* src = reinterpret_cast<const f32x4*>(
           cy.st_in + (size_t)min(m0 + (int)threadIdx.x, M - 1) * kMaxCarryTiles);
@@ -616,9 +628,28 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 #pragma unroll
     for (int fn = 0; fn < C::FN; ++fn) load_cols(fn, fn);
   }
+  float2* rmr = reinterpret_cast<float2*>(red);    // kResStats: [BM] (mean, rstd)
+  f16* rgb = reinterpret_cast<f16*>(red + 2 * C::BM);  // kResStats: [2][BN] gamma, beta
+  if constexpr (EPI == kResStats) {
+    static_assert(C::RED >= (2 * C::BM) * sizeof(float) + 2 * C::BN * sizeof(f16),
+                  "row statistics and gamma / beta fit the partials area");
+    if constexpr (!kCarryAhead) load_carry();
+    if (cy.mr_in) {  // read by the store threads after the tile pass's barrier
+      if (threadIdx.x < C::BM) rmr[threadIdx.x] = smr;
+      if (threadIdx.x < C::BN) {
+        rgb[threadIdx.x] = sg;
+        rgb[C::BN + threadIdx.x] = sb;
+      }
+    }
+  }
   if constexpr (kFoldE) {
     // Each row's (mean, rstd) once, by its loader thread, into the LayerNorm
-    // partials area (free for these epilogues), then to every lane of the row.
+    // partials area (free for these epilogues), then to every lane of the
+    // row; fs / fc after them.
+    static_assert((size_t)(C::BM / C::NPASS) * C::OUT_LD * sizeof(f16) +
+                          (2 * C::BM + 2 * C::BN) * sizeof(float) <= C::LDS,
+                  "row statistics and column operands fit beside the output tile");
+    float* fc_lds = red + 2 * C::BM;
     if (threadIdx.x < C::BM) {
       const float2 st = carried_row_stats(rp, eps);
       red[2 * threadIdx.x] = st.x;
@@ -626,6 +657,11 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       const int m = m0 + (int)threadIdx.x;
       if (ni == 0 && m < M && cy.mr_out) cy.mr_out[m] = st;
     }
+    if (threadIdx.x < C::BN) {
+      fc_lds[threadIdx.x] = cs;
+      fc_lds[C::BN + threadIdx.x] = cc;
+    }
+    fcol = fc_lds;
     lds_barrier();
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
@@ -771,7 +807,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
     }
     lds_barrier();
     if constexpr (EPI == kResStats)
-      store_rows_stats<C, PR>(tile, out, M, m0 + p * PR, n0, residual, gamma, beta, cy,
+      store_rows_stats<C, PR>(tile, out, M, m0 + p * PR, n0, residual, rmr + p * PR, rgb, cy,
                               kAhead ? &ahead : nullptr);
     else
       store_rows<C, PR>(tile, out, N, M, m0 + p * PR, n0, EPI == kResidual ? residual : nullptr,

@@ -1324,9 +1324,12 @@ const char* tile_name(int id) {
 // tried for each (shape, M) with the others fixed in the per-batch pass, then
 // the winners confirmed in interleaved repeats: FFN1 takes the 128x128
 // register-staged tile (30) from 1025 rows and FFN2 the 64x128 copy-ring tile
-// (1) from 2049 rows, 391K -> 409K sentences/s for the pass on three streams;
-// a sweep on four found no tile ahead of these.  There the other forwards
-// fill the CUs, and fewer, larger tiles move fewer bytes L2 -> CU per FLOP.
+// (1) from 2049 rows, 391K -> 409K sentences/s for the pass on three streams.
+// With the LayerNorms carried as row statistics (the epilogues heavier), a
+// sweep on four slots moved O-proj to tile 1 as well and QKV to tile 30 up to
+// 4096 rows: pass 4.144-4.160 -> 4.064-4.095 ms in four interleaved repeats.
+// There the other forwards fill the CUs, and fewer, larger tiles move fewer
+// bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K, bool shared) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
@@ -1335,9 +1338,9 @@ int pick_plain(int M, int N, int K, bool shared) {
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : !shared ? 34 : wide_k ? 1 : 0;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : !shared ? 34 : 1;
   else if (M <= 4096)
-    id = qkv ? 32 : ffn1 ? 30 : !shared ? 34 : wide_k ? 1 : 0;
+    id = qkv ? (shared ? 30 : 32) : ffn1 ? 30 : !shared ? 34 : 1;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

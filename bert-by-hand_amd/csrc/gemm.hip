@@ -1315,7 +1315,8 @@ const char* tile_name(int id) {
 // configs[1] and one-slot configs[3] forwards with one GEMM's tile changed at
 // a time: QKV runs the 64x64 copy-ring tile (0) up to 1024 rows (configs[1]
 // forward 230.1 -> 224.3 us: 288 workgroups instead of 72); FFN1 keeps that
-// tile to 2048 rows and the 64x64 register-staged one (26) to 3072; O-proj
+// tile to 4096 rows (with the LayerNorm carried in: one-slot pass 8.22-8.24
+// -> 8.11 ms against the register-staged 64x64 at 2049-3072 rows); O-proj
 // and FFN2 from 2049 rows run the 64x64 copy ring with two K slices per
 // barrier (34; one-slot varlen pass 9.00-9.03 -> 8.84-8.95 ms).  More
 // workgroups than CUs keep every CU busy, and the deeper rings fit beside
@@ -1338,9 +1339,9 @@ int pick_plain(int M, int N, int K, bool shared) {
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? (shared ? 30 : 26) : !shared ? 34 : 1;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : 1;
   else if (M <= 4096)
-    id = qkv ? (shared ? 30 : 32) : ffn1 ? 30 : !shared ? 34 : 1;
+    id = qkv ? (shared ? 30 : 32) : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : 1;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

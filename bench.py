@@ -350,10 +350,11 @@ def op_tags(rows, queue_col, grid):
     for r in order:
         q, k = r[queue_col], short_kernel(r["Kernel_Name"])
         p = prev.get(q)
-        if re.match(r"gemm_(kernel<.*, [23]>|wres_kernel<3>)$", k) and p:
+        # residual epilogues 2, 3, 6 (row statistics out); GELU epilogues 1, 5
+        if re.match(r"gemm_(kernel<.*, [236]>|wres_kernel<3>)$", k) and p:
             if p.startswith("attention_kernel"):
                 tags[r["Dispatch_Id"]] = " [o_proj]"
-            elif re.match(r"gemm_(kernel<.*, 1>|wres_kernel<1>)$", p):
+            elif re.match(r"gemm_(kernel<.*, [15]>|wres_kernel<1>)$", p):
                 tags[r["Dispatch_Id"]] = " [ffn2]"
         prev[q] = k
     return tags

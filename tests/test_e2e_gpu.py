@@ -146,6 +146,65 @@ def test_peaked_attention_end_to_end(torch_cuda, ws, weights32):
         model.close()
 
 
+def test_carried_layernorm_general_gamma_beta(torch_cuda, ws, weights32):
+    # The seeded weights have every LayerNorm at gamma 1, beta 0, where the
+    # carried LayerNorm's folded operands reduce to W itself and the bias.
+    # Here every gamma is drawn from [0.5, 1.5] and every beta from
+    # N(0, 0.1), so the forwards of at most 8192 rows run on W diag(gamma)
+    # copies with fc = W . beta + bias.  Against the oracle on the same
+    # weights: bert_encode's final rows and bert_embed's embeddings, carried
+    # (batch 24 x seq 64, M = 1,536) and with the LayerNorms in the GEMM
+    # epilogues (batch 40 x seq 256, M = 10,240); and the carried final rows
+    # against the layer-by-layer block entry points (LayerNorm passes, the
+    # reference's order of operations): no further from the oracle than they.
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    rng = np.random.default_rng(31)
+    w = {}
+    for k, v in weights32.items():
+        if k.endswith("LayerNorm.weight"):
+            v = rng.uniform(0.5, 1.5, size=v.shape).astype(np.float32)
+        elif k.endswith("LayerNorm.bias"):
+            v = (rng.standard_normal(v.shape) * 0.1).astype(np.float32)
+        w[k] = v
+    model = engine.Model.from_weights(w)
+    try:
+        short = synth.pack([synth.sentence(rng, int(n)) for n in rng.integers(5, 65, size=24)], 64)
+        long = synth.pack([synth.sentence(rng, int(n)) for n in rng.integers(100, 257, size=40)], 256)
+        for ids, types, mask in (short, long):
+            B, S = ids.shape
+            dev = [to_dev(torch, a) for a in (ids, types, mask)]
+            enc = _np(engine.bert_encode(ws, model, *dev)).reshape(B, S, 384)
+            want = O.bert_encode(w, ids, types, mask)
+            real = mask.astype(bool)
+            assert cosine_rows(enc[real], want[real]).min() >= COS, (B, S)
+            err = np.abs(enc[real] - want[real])
+            assert err.mean() < 5e-3 and err.max() < 0.1, (B, S, err.mean(), err.max())
+            emb = _np(engine.bert_embed(ws, model, *dev))
+            assert cosine_rows(emb, O.bert_embed(w, ids, types, mask)).min() >= COS, (B, S)
+            if B * S <= 8192:  # carried: the same rows through the block entry points
+                hid = torch.empty((B * S, 384), dtype=torch.float16, device="cuda")
+                engine.launch_embedding_layernorm(
+                    dev[0], dev[1], *(to_dev(torch, w[f"embeddings.{n}"].astype(np.float16))
+                                      for n in ("word_embeddings.weight",
+                                                "position_embeddings.weight",
+                                                "token_type_embeddings.weight",
+                                                "LayerNorm.weight", "LayerNorm.bias")),
+                    hid, S, batch=B)
+                for layer in range(6):
+                    out = torch.empty_like(hid)
+                    engine.encoder_layer(ws, model, layer, hid, dev[2], out, B, S)
+                    hid = out
+                blocks = _np(hid).reshape(B, S, 384)
+                assert cosine_rows(enc[real], blocks[real]).min() >= COS
+                err_blocks = np.abs(blocks[real] - want[real])
+                assert err.mean() <= 1.1 * err_blocks.mean(), (err.mean(), err_blocks.mean())
+                assert err.max() <= 1.5 * err_blocks.max(), (err.max(), err_blocks.max())
+    finally:
+        model.close()
+
+
 def test_workspace_hidden_is_final_hidden(torch_cuda, ws, model, golden_model):
     from bbh import engine
 

@@ -217,6 +217,10 @@ def launch_work(r):
         return 0.0, M * 1536.0 + 1536
     if op == "ffn":  # (M, 384, 1536): both Linears; X in (also the residual), out, weights
         return 4.0 * M * N * K, (2 * M * N + 2 * N * K + K + 3 * N) * 2.0
+    if op == "qkv" and r.get("fused_ln") == 3:  # QKV Linear + attention, (M, batch, seq)
+        B, S = N, K
+        flops = 2.0 * M * 1152 * 384 + 4.0 * B * 12 * 32 * S * S
+        return flops, (M * 384 * 2 + 1152 * 384 + M * 384) * 2.0 + B * S * 4.0 + M * 56.0
     flops = 2.0 * M * N * K
     byts = (M * K + N * K + M * N + N) * 2.0
     if op in ("o_proj_ln", "ffn2_ln"):
@@ -233,6 +237,8 @@ def kernel_name(engine, op, tile, fused):
            "ffn": "ffn_fused_kernel"}
     if op in row:
         return row[op], row[op]
+    if op == "qkv" and fused == 3:
+        return "qkv_attention_kernel", "qkv_attention_kernel"
     if fused == 2:  # the LayerNorm carried between the GEMMs as row statistics
         epi = {"qkv": "4 (carried LayerNorm in)", "ffn1_gelu": "5 (carried LayerNorm in+GELU)"}.get(
             op, "6 (bias+residual, row statistics out)")

@@ -135,6 +135,11 @@ struct bbh_model {
     // ones), fs = row sums of W', fc = W . beta + bias.
     const f16 *qkv_wf = nullptr, *f1_wf = nullptr;
     const float *qkv_fs = nullptr, *qkv_fc = nullptr, *f1_fs = nullptr, *f1_fc = nullptr;
+    // The QKV Linear of bbh::qkv_attention: qkv_wf (or qkv_w in layer 0) in
+    // head-major row order, its fs (none in layer 0) and fc (the bias in
+    // layer 0) in the same order.
+    const f16* qkv_wp = nullptr;
+    const float *qkv_fsp = nullptr, *qkv_fcp = nullptr;
   } layers[BBH_NUM_LAYERS];
 };
 
@@ -238,6 +243,14 @@ bbh_status fold_operands(const std::vector<uint16_t>& host, bbh_model* m) {
       cur = align256(cur + folds[f].n * H * sizeof(f16));
     }
   }
+  // Head-major QKV operands per layer: W (row h*96 + part*32 + d from row
+  // part*384 + h*32 + d), fs, fc.
+  std::vector<size_t> hm_at(BBH_NUM_LAYERS);
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    hm_at[i] = cur;
+    cur = align256(cur + 3 * H * H * sizeof(f16));
+    cur = align256(cur + 2 * 3 * H * sizeof(float));
+  }
   std::vector<unsigned char> buf(cur, 0);
   for (size_t f = 0; f < folds.size(); ++f) {
     const Fold& fd = folds[f];
@@ -261,6 +274,34 @@ bbh_status fold_operands(const std::vector<uint16_t>& host, bbh_model* m) {
       fc[n] = (float)(cc + (double)f16_bits_to_float(bias[n]));
     }
   }
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    const int b0 = kEmbParams + i * kPerLayer;
+    const uint16_t* W = host.data() + L.off[b0 + 0];  // Q | K | V rows
+    const uint16_t* bias = host.data() + L.off[b0 + 1];
+    const f16* wf = nullptr;  // the folded copy, where gamma is not all ones
+    const float *fs = nullptr, *fc = nullptr;
+    for (size_t f = 0; f < folds.size(); ++f)
+      if (folds[f].qkv && folds[f].layer == i) {
+        fs = reinterpret_cast<const float*>(buf.data() + vec_at[f]);
+        fc = fs + folds[f].n;
+        if (!ones[f]) wf = reinterpret_cast<const f16*>(buf.data() + w_at[f]);
+      }
+    f16* wp = reinterpret_cast<f16*>(buf.data() + hm_at[i]);
+    float* fsp = reinterpret_cast<float*>(buf.data() + align256(hm_at[i] + 3 * H * H * sizeof(f16)));
+    float* fcp = fsp + 3 * H;
+    for (size_t h = 0; h < (size_t)BBH_NUM_HEADS; ++h)
+      for (size_t part = 0; part < 3; ++part)
+        for (size_t d = 0; d < (size_t)BBH_HEAD_DIM; ++d) {
+          const size_t dst = h * 3 * BBH_HEAD_DIM + part * BBH_HEAD_DIM + d;
+          const size_t src = part * H + h * BBH_HEAD_DIM + d;
+          if (wf)
+            memcpy(wp + dst * H, wf + src * H, H * sizeof(f16));
+          else
+            memcpy(wp + dst * H, W + src * H, H * sizeof(f16));
+          fsp[dst] = fs ? fs[src] : 0.f;
+          fcp[dst] = fc ? fc[src] : f16_bits_to_float(bias[src]);
+        }
+  }
   void* dev = nullptr;
   BBH_HIP(hipMalloc(&dev, cur), "hipMalloc(carried LayerNorm operands)");
   const hipError_t e = hipMemcpy(dev, buf.data(), cur, hipMemcpyHostToDevice);
@@ -271,6 +312,12 @@ bbh_status fold_operands(const std::vector<uint16_t>& host, bbh_model* m) {
   m->fold_blob = dev;
   m->fold_bytes = cur;
   const unsigned char* base = static_cast<const unsigned char*>(dev);
+  for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
+    auto& l = m->layers[i];
+    l.qkv_wp = reinterpret_cast<const f16*>(base + hm_at[i]);
+    l.qkv_fsp = reinterpret_cast<const float*>(base + align256(hm_at[i] + 3 * H * H * sizeof(f16)));
+    l.qkv_fcp = l.qkv_fsp + 3 * H;
+  }
   for (size_t f = 0; f < folds.size(); ++f) {
     auto& l = m->layers[folds[f].layer];
     const float* fs = reinterpret_cast<const float*>(base + vec_at[f]);
@@ -530,13 +577,19 @@ bbh_status run_ffn_block(bbh_workspace* ws, const bbh_model::Layer& L, const f16
 // layer writes final_out (which may be ws->attn_out: each residual chunk is
 // read by the thread that then overwrites it); its ln2 follows as a pass over
 // final_out, or is left to the caller (final_ln_deferred).  Timing records
-// of the carried GEMMs have fused_ln 2.
+// of the carried GEMMs have fused_ln 2, and of bbh::qkv_attention (one padded
+// segment, seq <= 128) fused_ln 3 with (M, batch, seq).
 bbh_status run_layers_carried(bbh_workspace* ws, const bbh_model* m, f16* h0, const Segment* segs,
                               int n_segs, const Packed* pk, int M, f16* final_out, hipStream_t s,
                               OpTimer* t, bool* final_ln_deferred) {
   const int H = BBH_HIDDEN, F = BBH_FFN_DIM;
   const float eps = BBH_LAYER_NORM_EPS;
   const bool sh = ws->shared;
+  // One padded segment of at most 128 tokens a sentence: QKV and attention
+  // as one kernel.
+  const bool fused_qa = !pk && n_segs == 1 && segs[0].row == 0 &&
+                        bbh::qkv_attention_ok(segs[0].batch, segs[0].seq) &&
+                        aligned(segs[0].mask, 4);
   const f16* cur = h0;
   for (int i = 0; i < BBH_NUM_LAYERS; ++i) {
     const bbh_model::Layer& L = m->layers[i];
@@ -544,7 +597,20 @@ bbh_status run_layers_carried(bbh_workspace* ws, const bbh_model* m, f16* h0, co
     const bool last = i == BBH_NUM_LAYERS - 1;
     f16* nxt = last ? final_out : (cur == ws->ping ? ws->pong : ws->ping);
     const int qkv_tile = bbh::gemm_tile(M, 3 * H, H, sh);
-    if (!P) {
+    if (fused_qa) {
+      // QKV Linear and attention in one kernel (timing record: fused_ln 3)
+      bbh::LnCarry cy;
+      if (P) {
+        cy.st_in = ws->st_b;
+        cy.mr_out = ws->mr_b;
+      }
+      BBH_TRY(timed_op(t, s, {BBH_OP_QKV, -1, 3, M, segs[0].batch, segs[0].seq, 0.f}, [&] {
+        return check_launch(bbh::qkv_attention(cur, L.qkv_wp, L.qkv_fsp, L.qkv_fcp, cy,
+                                               segs[0].mask, ws->ctx, segs[0].batch,
+                                               segs[0].seq, kScale, eps, s),
+                            "qkv + attention");
+      }));
+    } else if (!P) {
       BBH_TRY(timed_op(t, s, {BBH_OP_QKV, qkv_tile, 0, M, 3 * H, H, 0.f}, [&] {
         return check_launch(bbh::gemm(cur, L.qkv_w, L.qkv_b, ws->qkv, M, 3 * H, H,
                                       bbh::Act::kNone, s, sh),
@@ -562,7 +628,7 @@ bbh_status run_layers_carried(bbh_workspace* ws, const bbh_model* m, f16* h0, co
                             "qkv gemm (carried LayerNorm)");
       }));
     }
-    BBH_TRY(run_attention(ws, segs, n_segs, s, t, pk));
+    if (!fused_qa) BBH_TRY(run_attention(ws, segs, n_segs, s, t, pk));
     bool fused;
     {
       bbh::LnCarry cy;

@@ -816,6 +816,216 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
   }
 }
 
+// ---- QKV Linear and attention in one kernel (forwards of up to 8192 rows) --
+// A batch-64 forward spends about a tenth of its time in attention launches
+// whose work is a few hundred cycles: one global round trip for Q, K and V
+// just written by the QKV Linear, then the launch's tail.  Here workgroup
+// (group of G = 128 / seq sentences, head h) computes the QKV Linear's 96
+// columns of head h over the group's rows (a head-major copy of W: rows
+// h*96 .. h*96+95 are Q, K, V of head h), with the bias or carried-LayerNorm
+// epilogue of gemm_fold, writes them to LDS as Q rows, K rows (the attention
+// kernel's swizzled layout) and V^T, and runs each sentence's masked
+// attention from there, the arithmetic of attention_kernel with one query
+// tile per wavefront: the same bits as the two kernels.
+namespace qa {
+using C = Cfg<128, 96, 4, 1, 2, 0, 2>;
+constexpr int BM = 128, KR = BM + 32, VLD = KR + 8, HD = kHeadDim, NQ = 3 * HD;
+constexpr float kLazy = 8.f;  // as attention_kernel: the running max may lag by 2^8
+// LDS after the K loop (bytes): Q [BM][32], K [KR][32] (swizzled), V^T
+// [32][VLD], key bias [G][round32(seq)] (at most 256), row (mean, rstd)
+// [BM], fs / fc [2][96].
+constexpr size_t OFF_Q = 0, OFF_K = OFF_Q + (size_t)BM * HD * 2, OFF_V = OFF_K + (size_t)KR * HD * 2,
+                 OFF_B = OFF_V + (size_t)HD * VLD * 2, OFF_R = OFF_B + 256 * 4,
+                 OFF_F = OFF_R + (size_t)BM * 8, END = OFF_F + (size_t)2 * NQ * 4;
+constexpr size_t LDS = C::LDS > END ? C::LDS : END;
+static_assert(OFF_V % 16 == 0 && OFF_R % 16 == 0 && OFF_F % 16 == 0 && (VLD * 2) % 16 == 0, "align");
+__device__ __forceinline__ int key_of_row(int r) {
+  const int a = r >> 3, c = (r >> 2) & 1, b = r & 3;
+  return 16 * (a >> 1) + 8 * c + 4 * (a & 1) + b;
+}
+__device__ __forceinline__ int ks_off(int key, int c) { return key * 32 + ((c ^ ((key >> 2) & 3)) << 3); }
+}  // namespace qa
+
+__global__ __launch_bounds__(256) void qkv_attention_kernel(
+    const f16* __restrict__ X, const f16* __restrict__ Wp, const float* __restrict__ fs,
+    const float* __restrict__ fc, LnCarry cy, const int32_t* __restrict__ mask,
+    f16* __restrict__ ctx, int batch, int seq, int G, float c, float eps) {
+  using namespace qa;
+  HIP_DYNAMIC_SHARED(f16, smem);
+  const int x = blockIdx.x & 7, kx = blockIdx.x >> 3;
+  const int grp = (kx / kHeads) * 8 + x, h = kx % kHeads;
+  const int b0 = grp * G;
+  if (b0 >= batch) return;  // the whole workgroup: no barrier reached
+  const int gv = min(G, batch - b0), M = batch * seq, m0 = b0 * seq, R = gv * seq;
+  const int ntq = (seq + 31) >> 5, KP = ntq * 32;  // query tiles (key chunks) per sentence
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r32 = lane & 31, kh = lane >> 5;
+
+  // Before the K loop, so that their latency hides behind it: the six
+  // group pairs of tile row tid (carried LayerNorm), fs / fc of column tid,
+  // and the mask of (sentence tid / KP, key tid % KP).
+  float2 rp[kMaxCarryTiles];
+  if (cy.st_in && tid < BM) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(cy.st_in + (size_t)min(m0 + tid, M - 1) *
+                                                                     kMaxCarryTiles);
+#pragma unroll
+    for (int k = 0; k < kMaxCarryTiles / 2; ++k) {
+      const f32x4 v = src[k];
+      rp[2 * k] = make_float2(v[0], v[1]);
+      rp[2 * k + 1] = make_float2(v[2], v[3]);
+    }
+  }
+  float cs = 0.f, cc = 0.f;
+  if (tid < NQ) {
+    cs = fs ? fs[h * NQ + tid] : 0.f;
+    cc = fc[h * NQ + tid];
+  }
+  int mv = 0;
+  if (tid < gv * KP) {
+    const int g = tid / KP, key = tid - g * KP;
+    if (key < seq) mv = mask[(size_t)(b0 + g) * seq + key];
+  }
+
+  f32x16 acc[1][3];
+  mainloop<C>(X, Wp, M, kHidden, m0, h * NQ, smem, acc);
+
+  unsigned char* lds = reinterpret_cast<unsigned char*>(smem);
+  f16* Qs = reinterpret_cast<f16*>(lds + OFF_Q);
+  f16* Ks = reinterpret_cast<f16*>(lds + OFF_K);
+  f16* Vt = reinterpret_cast<f16*>(lds + OFF_V);
+  float* mb = reinterpret_cast<float*>(lds + OFF_B);
+  float2* rs = reinterpret_cast<float2*>(lds + OFF_R);
+  float* fcol = reinterpret_cast<float*>(lds + OFF_F);
+  if (tid < BM) {
+    float2 st = make_float2(0.f, 1.f);  // no carried LayerNorm: acc + bias
+    if (cy.st_in) {
+      st = carried_row_stats(rp, eps);
+      if (h == 0 && tid < R && cy.mr_out) cy.mr_out[m0 + tid] = st;
+    }
+    rs[tid] = st;
+  }
+  if (tid < NQ) {
+    fcol[tid] = cs;
+    fcol[NQ + tid] = cc;
+  }
+  if (tid < gv * KP) mb[tid] = mv != 0 ? 0.f : -INFINITY;
+  // K rows and V^T columns BM .. KR-1, which a sentence's last key chunk may
+  // reach past the group, hold zeros (their keys are masked).
+  for (int i = tid; i < (KR - BM) * HD; i += 256) {
+    Ks[BM * HD + i] = (f16)0.f;
+    Vt[(i / (KR - BM)) * VLD + BM + i % (KR - BM)] = (f16)0.f;
+  }
+  lds_barrier();
+  {
+    // Epilogue: acc[0][fn][4j+e] is column fn*32 + 8j + 4kh + e (Q, K, V of
+    // head h) of local row r, as gemm_fold computes it.
+    const int r = wave * 32 + r32;
+    const float2 st = rs[r];
+#pragma unroll
+    for (int fn = 0; fn < 3; ++fn)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d0 = 8 * j + 4 * kh;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(fcol + fn * HD + d0);
+        const f32x4 cv = *reinterpret_cast<const f32x4*>(fcol + NQ + fn * HD + d0);
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = to_half(fmaf(-st.x, sv[e], acc[0][fn][4 * j + e]) * st.y + cv[e]);
+        if (fn == 0) {
+          *reinterpret_cast<f16x4*>(Qs + r * HD + d0) = o;
+        } else if (fn == 1) {
+          *reinterpret_cast<f16x4*>(Ks + ks_off(r, j) + 4 * kh) = o;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) Vt[(d0 + e) * VLD + r] = o[e];
+        }
+      }
+  }
+  lds_barrier();
+
+  // Attention: query tile t of sentence g (rows g*seq + t*32 ..) per
+  // wavefront, over the sentence's key chunks.
+  const int krow = key_of_row(r32);
+  const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const f16x2 ones = {(f16)1.f, (f16)1.f};
+  const float lag = kLazy / c;
+  for (int qt = wave; qt < gv * ntq; qt += 4) {
+    const int g = qt / ntq, t = qt - g * ntq, kb = g * seq;
+    // Rows past the sentence read its last row (as attention_kernel clamps
+    // them), so they take the same rescale decisions; they are not stored.
+    const int qr = kb + min(t * 32 + r32, seq - 1);
+    const f16x8 q0 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 8 * kh);
+    const f16x8 q1 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 16 + 8 * kh);
+    const float* mbg = mb + g * KP;
+    f32x16 o = zero;
+    float m = 0.f, l = 0.f;
+    bool started = false;
+    for (int kc = 0; kc < ntq; ++kc) {
+      const uint32_t bits = (uint32_t)__ballot(mbg[kc * 32 + r32] == 0.f);
+      if (bits == 0) continue;  // every key of the chunk masked: contributes nothing
+      const int key = kb + kc * 32 + krow;
+      const f16x8 k0 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, kh));
+      const f16x8 k1 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, 2 + kh));
+      f32x16 sc = mfma32(k0, q0, zero);
+      sc = mfma32(k1, q1, sc);  // sc[i]: key kc*32 + 16*(i/8) + 8*kh + i%8 (raw)
+      if (bits != 0xffffffffu) {
+        const float* mk = mbg + kc * 32 + 8 * kh;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[i] += mk[16 * (i >> 3) + (i & 7)];
+      }
+      float v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[0], sc[1]), sc[2]);
+#pragma unroll
+      for (int i = 3; i < 15; i += 2)
+        v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(v, sc[i]), sc[i + 1]);
+      v = __builtin_elementwise_maximum(v, sc[15]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                       false, false);
+      const float mx = __builtin_elementwise_maximum(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const bool up = mx > m + lag;
+      if (!started) {
+        m = mx;
+        started = true;
+      } else if (__ballot(up)) {
+        const float mn = fmaxf(m, mx);
+        const float corr = __builtin_amdgcn_exp2f((m - mn) * c);
+        l *= corr;
+        o *= corr;
+        m = mn;
+      }
+      const f16* vrow = Vt + r32 * VLD + kb + kc * 32 + 8 * kh;
+      const f16x8 va = *reinterpret_cast<const f16x8*>(vrow);
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(vrow + 16);
+      const float mc = m * c;
+      f16x8 pa, pb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pa[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[i], c, -mc));
+        pb[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[8 + i], c, -mc));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        l = __builtin_amdgcn_fdot2(f16x2{pa[i], pa[i + 1]}, ones, l, false);
+        l = __builtin_amdgcn_fdot2(f16x2{pb[i], pb[i + 1]}, ones, l, false);
+      }
+      o = mfma32(va, pa, o);
+      o = mfma32(vb, pb, o);
+    }
+    const float lt = xor32_sum(l);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    const int q = t * 32 + r32;
+    if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
+      f16* dst = ctx + (size_t)(m0 + kb + q) * kHidden + h * HD + 4 * kh;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
+        *reinterpret_cast<f16x4*>(dst + 8 * j) = w;
+      }
+    }
+  }
+}
+
 // ---- Weight-resident kernel for K = 384 -----------------------------------
 // The QKV and FFN1 Linears have K = 384, so one wavefront can hold the fp16 W
 // fragments of 32 output columns for the whole K in 96 VGPRs.  A workgroup of
@@ -1439,6 +1649,28 @@ hipError_t launch_carry(int id, const f16* A, const f16* W, const f16* bias, con
 }
 
 bool ln_carry_ok(int M) { return M >= 1 && M <= 8192; }
+
+bool qkv_attention_ok(int batch, int seq) {
+  return batch >= 1 && seq >= 16 && seq <= 128 && seq % 16 == 0 && ln_carry_ok(batch * seq);
+}
+
+hipError_t qkv_attention(const f16* X, const f16* Wp, const float* fs, const float* fc,
+                         const LnCarry& cy, const int32_t* mask, f16* ctx, int batch, int seq,
+                         float scale, float eps, hipStream_t s) {
+  const bool aligned = (((uintptr_t)X | (uintptr_t)Wp | (uintptr_t)ctx) & 15) == 0 &&
+                       (((uintptr_t)cy.st_in) & 15) == 0;
+  if (!qkv_attention_ok(batch, seq) || !fc || !mask || !aligned) return hipErrorInvalidValue;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_attention_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)qa::LDS);
+  if (attr != hipSuccess) return attr;
+  const int G = qa::BM / seq, groups = (batch + G - 1) / G;
+  const int grid = kHeads * 8 * ((groups + 7) / 8);
+  const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
+  hipLaunchKernelGGL(qkv_attention_kernel, dim3(grid), dim3(256), qa::LDS, s, X, Wp, fs, fc, cy, mask,
+                     ctx, batch, seq, G, c, eps);
+  return hipGetLastError();
+}
 
 hipError_t gemm_fold(const f16* A, const f16* W, const LnCarry& cy, f16* C, int M, int N, int K,
                      Act act, float eps, hipStream_t s, bool shared) {

@@ -57,6 +57,18 @@ hipError_t gemm_residual_stats(const f16* A, const f16* W, const f16* bias, cons
                                const f16* gamma, const f16* beta, const LnCarry& cy, f16* y,
                                int M, int K, hipStream_t s, bool shared = false);
 
+// The QKV Linear and masked attention of a padded batch in one kernel
+// (qkv_attention_ok: seq a multiple of 16 up to 128, batch*seq <= 8192):
+// ctx (merged heads) from the hidden rows X.  Wp is the QKV weight in
+// head-major row order (rows h*96 .. h*96+95: Q, K, V of head h), fs / fc
+// per column in the same order; the epilogue is gemm_fold's with the input
+// rows' statistics from cy (st_in, and mr_out written) or, without st_in,
+// acc + fc (fc the bias).  The same bits as that Linear and attention().
+bool qkv_attention_ok(int batch, int seq);
+hipError_t qkv_attention(const f16* X, const f16* Wp, const float* fs, const float* fc,
+                         const LnCarry& cy, const int32_t* mask, f16* ctx, int batch, int seq,
+                         float scale, float eps, hipStream_t s);
+
 // Tile configuration gemm() / gemm_residual_ln() launch for a shape (-1: the
 // plain tiled kernel), whether the LayerNorm is inside the GEMM kernel, and
 // the configuration's name as it appears in the kernel symbol.

@@ -317,6 +317,32 @@ def test_pool_embed_batches_equals_sequential(torch_cuda, ws, model):
     pool.close()
 
 
+def test_qkv_attention_kernel_equals_two_kernels(torch_cuda, ws, model):
+    # bert_embed on one padded batch of at most 8192 rows and seq <= 128 runs
+    # the QKV Linear and attention as one kernel (bbh::qkv_attention); a
+    # forward over several padded segments (bbh_embed_batches packing the
+    # varlen batches into groups of up to 8192 rows on one slot) runs them as
+    # the QKV GEMM and attention_kernel, with the same carried LayerNorms:
+    # the same bits.  Also at seq 128 and 16 (configs[1] / configs[2] rows).
+    from bbh import engine, synth
+
+    torch = torch_cuda
+    batches = synth.varlen_mix()[:12]
+    rng = np.random.default_rng(41)
+    for S, B in ((128, 24), (16, 40)):
+        n = rng.integers(1, S + 1, size=B)
+        mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
+        ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)
+        batches.append((ids, np.zeros_like(ids), mask, S))
+    pool = engine.Pool(1, 64, 128)  # 8,192 rows: groups of several segments, carried LayerNorms
+    packed = engine.PackedBatches([b[:3] for b in batches])
+    got = _np(engine.embed_batches(pool, model, packed))
+    torch.cuda.synchronize()
+    pool.close()
+    want = np.concatenate([_embed(torch, ws, model, *b[:3]) for b in batches])
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("max_batch", [256, 1024])
 def test_pool_merges_equal_seq_batches(torch_cuda, ws, model, max_batch):
     # Length-grouped packing: each run of equal-seq batches executes as one
@@ -400,7 +426,9 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
             engine.embed_each(pool, model, packed)
             recs = pool.timing_read()
             pool.timing(0)
-            assert len(recs) > 6 * 40 and all(r["ms"] > 0 for r in recs)
+            # at least embedding + 6 x (QKV with attention, O-proj, FFN1,
+            # FFN2) + pool a forward
+            assert len(recs) >= 26 * len(batches) and all(r["ms"] > 0 for r in recs)
         pool.close()
     # bert_embed's workspace: the final hidden rows are LayerNorm outputs
     ids, types, mask = batches[4]

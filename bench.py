@@ -358,7 +358,7 @@ def op_tags(rows, queue_col, grid):
         p = prev.get(q)
         # residual epilogues 2, 3, 6 (row statistics out); GELU epilogues 1, 5
         if re.match(r"gemm_(kernel<.*, [236]>|wres_kernel<3>)$", k) and p:
-            if p.startswith("attention_kernel"):
+            if p.startswith(("attention_kernel", "qkv_attention_kernel")):
                 tags[r["Dispatch_Id"]] = " [o_proj]"
             elif re.match(r"gemm_(kernel<.*, [15]>|wres_kernel<1>)$", p):
                 tags[r["Dispatch_Id"]] = " [ffn2]"

@@ -298,7 +298,10 @@ typedef enum bbh_op {
 typedef struct bbh_launch_time {
   int op;       /* bbh_op */
   int tile;     /* GEMM tile configuration (bbh_gemm_tile_name); -1 for other ops */
-  int fused_ln; /* 2: the LayerNorm carried as row statistics (forwards of at most 8192 rows):
+  int fused_ln; /* 3 (BBH_OP_QKV only): the QKV Linear and the attention in one kernel (padded
+                   forwards of at most 8192 rows and 128 tokens a sentence); no
+                   BBH_OP_ATTENTION record follows, and m, n, k are (rows, batch, seq).
+                   2: the LayerNorm carried as row statistics (forwards of at most 8192 rows):
                    O-proj / FFN2 write the rows before it with their statistics and no pass
                    follows; QKV (from layer 1) / FFN1 normalise their input rows from them.
                    O-proj / FFN2: 1 when the LayerNorm runs inside the GEMM kernel, 0 when it

@@ -1538,7 +1538,9 @@ const char* tile_name(int id) {
 // (1) from 2049 rows, 391K -> 409K sentences/s for the pass on three streams.
 // With the LayerNorms carried as row statistics (the epilogues heavier), a
 // sweep on four slots moved O-proj to tile 1 as well and QKV to tile 30 up to
-// 4096 rows: pass 4.144-4.160 -> 4.064-4.095 ms in four interleaved repeats.
+// 4096 rows: pass 4.144-4.160 -> 4.064-4.095 ms in four interleaved repeats;
+// with QKV inside the attention kernel, O-proj to the 128x128 tile (30):
+// 4.117-4.127 -> 4.092-4.104 ms.
 // There the other forwards fill the CUs, and fewer, larger tiles move fewer
 // bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K, bool shared) {
@@ -1549,9 +1551,9 @@ int pick_plain(int M, int N, int K, bool shared) {
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : 26;
   else if (M <= 3072)
-    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : 1;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : wide_k ? 1 : 30;
   else if (M <= 4096)
-    id = qkv ? (shared ? 30 : 32) : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : 1;
+    id = qkv ? (shared ? 30 : 32) : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : wide_k ? 1 : 30;
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)

@@ -67,7 +67,7 @@ struct Cfg {
   static constexpr int NPASS = ((size_t)BM * OUT_LD * sizeof(f16) + RED <= kLdsMax) ? 1 : WM;
   static constexpr size_t OUT = (size_t)(BM / NPASS) * OUT_LD * sizeof(f16) + RED;
   static constexpr size_t LDS = RING > OUT ? RING : OUT;
-  static_assert(NW == 4 || NW == 8, "four or eight wavefronts");
+  static_assert(NW == 4 || NW == 6 || NW == 8, "four, six or eight wavefronts");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile is whole 32x32 blocks");
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "load distribution");
   static_assert(SA >= 2 && SW >= 2, "ring depths");
@@ -828,17 +828,28 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 // attention from there, the arithmetic of attention_kernel with one query
 // tile per wavefront: the same bits as the two kernels.
 namespace qa {
-using C = Cfg<128, 96, 4, 1, 2, 0, 2>;
-constexpr int BM = 128, KR = BM + 32, VLD = KR + 8, HD = kHeadDim, NQ = 3 * HD;
+constexpr int HD = kHeadDim, NQ = 3 * HD;
 constexpr float kLazy = 8.f;  // as attention_kernel: the running max may lag by 2^8
-// LDS after the K loop (bytes): Q [BM][32], K [KR][32] (swizzled), V^T
-// [32][VLD], key bias [G][round32(seq)] (at most 256), row (mean, rstd)
-// [BM], fs / fc [2][96].
-constexpr size_t OFF_Q = 0, OFF_K = OFF_Q + (size_t)BM * HD * 2, OFF_V = OFF_K + (size_t)KR * HD * 2,
-                 OFF_B = OFF_V + (size_t)HD * VLD * 2, OFF_R = OFF_B + 256 * 4,
-                 OFF_F = OFF_R + (size_t)BM * 8, END = OFF_F + (size_t)2 * NQ * 4;
-constexpr size_t LDS = C::LDS > END ? C::LDS : END;
-static_assert(OFF_V % 16 == 0 && OFF_R % 16 == 0 && OFF_F % 16 == 0 && (VLD * 2) % 16 == 0, "align");
+// A workgroup of BM / 32 wavefronts over BM rows (128, or 192 where a
+// sentence length fills it better).  LDS after the K loop (bytes): Q
+// [BM][32], K [KR][32] (swizzled), V^T [32][VLD], key bias [G][round32(seq)]
+// (at most 384), row (mean, rstd) [BM], fs / fc [2][96].
+template <int BM_>
+struct Layout {
+  static constexpr int BM = BM_, NWV = BM / 32, NT = 64 * NWV, KR = BM + 32, VLD = KR + 8, MBN = 384;
+  using C = Cfg<BM, NQ, NWV, 1, 2, 0, 2>;
+  static constexpr size_t OFF_Q = 0, OFF_K = OFF_Q + (size_t)BM * HD * 2,
+                          OFF_V = OFF_K + (size_t)KR * HD * 2, OFF_B = OFF_V + (size_t)HD * VLD * 2,
+                          OFF_R = OFF_B + (size_t)MBN * 4, OFF_F = OFF_R + (size_t)BM * 8,
+                          END = OFF_F + (size_t)2 * NQ * 4;
+  static constexpr size_t LDS = C::LDS > END ? C::LDS : END;
+  static_assert(OFF_V % 16 == 0 && OFF_R % 16 == 0 && OFF_F % 16 == 0 && (VLD * 2) % 16 == 0,
+                "align");
+  static_assert(NT >= BM && NT >= NQ, "a thread per tile row / column");
+};
+// Rows a workgroup takes for a sentence length: 192 where 128 would leave a
+// quarter or more of the tile idle (seq 48, 80, 96).
+inline int rows_for(int seq) { return (seq == 48 || seq == 80 || seq == 96) ? 192 : 128; }
 __device__ __forceinline__ int key_of_row(int r) {
   const int a = r >> 3, c = (r >> 2) & 1, b = r & 3;
   return 16 * (a >> 1) + 8 * c + 4 * (a & 1) + b;
@@ -846,11 +857,15 @@ __device__ __forceinline__ int key_of_row(int r) {
 __device__ __forceinline__ int ks_off(int key, int c) { return key * 32 + ((c ^ ((key >> 2) & 3)) << 3); }
 }  // namespace qa
 
-__global__ __launch_bounds__(256) void qkv_attention_kernel(
+template <int BM_>
+__global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
     const f16* __restrict__ X, const f16* __restrict__ Wp, const float* __restrict__ fs,
     const float* __restrict__ fc, LnCarry cy, const int32_t* __restrict__ mask,
     f16* __restrict__ ctx, int batch, int seq, int G, float c, float eps) {
   using namespace qa;
+  using L = Layout<BM_>;
+  using C = typename L::C;
+  constexpr int BM = L::BM, KR = L::KR, VLD = L::VLD, NT = L::NT;
   HIP_DYNAMIC_SHARED(f16, smem);
   const int x = blockIdx.x & 7, kx = blockIdx.x >> 3;
   const int grp = (kx / kHeads) * 8 + x, h = kx % kHeads;
@@ -889,12 +904,12 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(
   mainloop<C>(X, Wp, M, kHidden, m0, h * NQ, smem, acc);
 
   unsigned char* lds = reinterpret_cast<unsigned char*>(smem);
-  f16* Qs = reinterpret_cast<f16*>(lds + OFF_Q);
-  f16* Ks = reinterpret_cast<f16*>(lds + OFF_K);
-  f16* Vt = reinterpret_cast<f16*>(lds + OFF_V);
-  float* mb = reinterpret_cast<float*>(lds + OFF_B);
-  float2* rs = reinterpret_cast<float2*>(lds + OFF_R);
-  float* fcol = reinterpret_cast<float*>(lds + OFF_F);
+  f16* Qs = reinterpret_cast<f16*>(lds + L::OFF_Q);
+  f16* Ks = reinterpret_cast<f16*>(lds + L::OFF_K);
+  f16* Vt = reinterpret_cast<f16*>(lds + L::OFF_V);
+  float* mb = reinterpret_cast<float*>(lds + L::OFF_B);
+  float2* rs = reinterpret_cast<float2*>(lds + L::OFF_R);
+  float* fcol = reinterpret_cast<float*>(lds + L::OFF_F);
   if (tid < BM) {
     float2 st = make_float2(0.f, 1.f);  // no carried LayerNorm: acc + bias
     if (cy.st_in) {
@@ -910,7 +925,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(
   if (tid < gv * KP) mb[tid] = mv != 0 ? 0.f : -INFINITY;
   // K rows and V^T columns BM .. KR-1, which a sentence's last key chunk may
   // reach past the group, hold zeros (their keys are masked).
-  for (int i = tid; i < (KR - BM) * HD; i += 256) {
+  for (int i = tid; i < (KR - BM) * HD; i += NT) {
     Ks[BM * HD + i] = (f16)0.f;
     Vt[(i / (KR - BM)) * VLD + BM + i % (KR - BM)] = (f16)0.f;
   }
@@ -949,7 +964,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(
   const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const f16x2 ones = {(f16)1.f, (f16)1.f};
   const float lag = kLazy / c;
-  for (int qt = wave; qt < gv * ntq; qt += 4) {
+  for (int qt = wave; qt < gv * ntq; qt += L::NWV) {
     const int g = qt / ntq, t = qt - g * ntq, kb = g * seq;
     // Rows past the sentence read its last row (as attention_kernel clamps
     // them), so they take the same rescale decisions; they are not stored.
@@ -1652,6 +1667,22 @@ hipError_t launch_carry(int id, const f16* A, const f16* W, const f16* bias, con
 
 bool ln_carry_ok(int M) { return M >= 1 && M <= 8192; }
 
+template <int BM>
+hipError_t launch_qkv_attention(const f16* X, const f16* Wp, const float* fs, const float* fc,
+                                const LnCarry& cy, const int32_t* mask, f16* ctx, int batch, int seq,
+                                float c, float eps, hipStream_t s) {
+  using L = qa::Layout<BM>;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_attention_kernel<BM>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)L::LDS);
+  if (attr != hipSuccess) return attr;
+  const int G = BM / seq, groups = (batch + G - 1) / G;
+  const int grid = kHeads * 8 * ((groups + 7) / 8);
+  hipLaunchKernelGGL(qkv_attention_kernel<BM>, dim3(grid), dim3(L::NT), L::LDS, s, X, Wp, fs, fc, cy,
+                     mask, ctx, batch, seq, G, c, eps);
+  return hipGetLastError();
+}
+
 bool qkv_attention_ok(int batch, int seq) {
   return batch >= 1 && seq >= 16 && seq <= 128 && seq % 16 == 0 && ln_carry_ok(batch * seq);
 }
@@ -1662,16 +1693,10 @@ hipError_t qkv_attention(const f16* X, const f16* Wp, const float* fs, const flo
   const bool aligned = (((uintptr_t)X | (uintptr_t)Wp | (uintptr_t)ctx) & 15) == 0 &&
                        (((uintptr_t)cy.st_in) & 15) == 0;
   if (!qkv_attention_ok(batch, seq) || !fc || !mask || !aligned) return hipErrorInvalidValue;
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(qkv_attention_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)qa::LDS);
-  if (attr != hipSuccess) return attr;
-  const int G = qa::BM / seq, groups = (batch + G - 1) / G;
-  const int grid = kHeads * 8 * ((groups + 7) / 8);
   const float c = scale * 1.4426950408889634f;  // scores * c are base-2 exponents
-  hipLaunchKernelGGL(qkv_attention_kernel, dim3(grid), dim3(256), qa::LDS, s, X, Wp, fs, fc, cy, mask,
-                     ctx, batch, seq, G, c, eps);
-  return hipGetLastError();
+  return qa::rows_for(seq) == 192
+             ? launch_qkv_attention<192>(X, Wp, fs, fc, cy, mask, ctx, batch, seq, c, eps, s)
+             : launch_qkv_attention<128>(X, Wp, fs, fc, cy, mask, ctx, batch, seq, c, eps, s);
 }
 
 hipError_t gemm_fold(const f16* A, const f16* W, const LnCarry& cy, f16* C, int M, int N, int K,

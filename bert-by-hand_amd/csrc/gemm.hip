@@ -833,10 +833,11 @@ constexpr float kLazy = 8.f;  // as attention_kernel: the running max may lag by
 // A workgroup of BM / 32 wavefronts over BM rows (128, or 192 where a
 // sentence length fills it better).  LDS after the K loop (bytes): Q
 // [BM][32], K [KR][32] (swizzled), V^T [32][VLD], key bias [G][round32(seq)]
-// (at most 384), row (mean, rstd) [BM], fs / fc [2][96].
+// (at most 2 BM), row (mean, rstd) [BM], fs / fc [2][96].
 template <int BM_>
 struct Layout {
-  static constexpr int BM = BM_, NWV = BM / 32, NT = 64 * NWV, KR = BM + 32, VLD = KR + 8, MBN = 384;
+  static constexpr int BM = BM_, NWV = BM / 32, NT = 64 * NWV, KR = BM + 32, VLD = KR + 8;
+  static constexpr int MBN = 2 * BM;  // >= G * round32(seq) for every seq, = NT
   using C = Cfg<BM, NQ, NWV, 1, 2, 0, 2>;
   static constexpr size_t OFF_Q = 0, OFF_K = OFF_Q + (size_t)BM * HD * 2,
                           OFF_V = OFF_K + (size_t)KR * HD * 2, OFF_B = OFF_V + (size_t)HD * VLD * 2,

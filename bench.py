@@ -230,15 +230,23 @@ def launch_work(r):
     return flops, byts
 
 
-def kernel_name(engine, op, tile, fused):
-    """(display name, class name as short_kernel() writes it) of a launch record."""
+def qkv_attention_rows(seq):
+    """Rows of a qkv_attention_kernel workgroup at this sentence length: 192 (six
+    wavefronts) for seq 48, 80 and 96, whose sentences fill 192 rows exactly, else 128."""
+    return 192 if seq in (48, 80, 96) else 128
+
+
+def kernel_name(engine, op, tile, fused, seq=0):
+    """(display name, class name as short_kernel() writes it) of a launch record;
+    seq: the sentence length of a fused QKV + attention record (its k)."""
     row = {"attention": "attention_kernel", "embed": "embedding_ln_kernel",
            "pool": "pool_normalize_kernel", "layernorm": "ln384_kernel",
            "ffn": "ffn_fused_kernel"}
     if op in row:
         return row[op], row[op]
     if op == "qkv" and fused == 3:
-        return "qkv_attention_kernel", "qkv_attention_kernel"
+        name = f"qkv_attention_kernel<{qkv_attention_rows(seq)}>"
+        return name, name
     if fused == 2:  # the LayerNorm carried between the GEMMs as row statistics
         epi = {"qkv": "4 (carried LayerNorm in)", "ffn1_gelu": "5 (carried LayerNorm in+GELU)"}.get(
             op, "6 (bias+residual, row statistics out)")
@@ -268,7 +276,7 @@ def classify(engine, recs, steps):
     algorithmic FLOPs and bytes, sorted by summed time."""
     classes = {}
     for r in recs:
-        key = (r["op"], r["tile"], r["fused_ln"], r["m"])
+        key = (r["op"], r["tile"], r["fused_ln"], r["m"], r["k"] if r["fused_ln"] == 3 else 0)
         c = classes.setdefault(key, {"ms": 0.0, "n": 0, "flops": 0.0, "bytes": 0.0, "m": set()})
         f, b = launch_work(r)
         c["ms"] += r["ms"]
@@ -278,9 +286,9 @@ def classify(engine, recs, steps):
         c["bytes"] += b
     total = sum(c["ms"] for c in classes.values())
     rows = []
-    for (op, tile, fused, m), c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
+    for (op, tile, fused, m, seq), c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
         avg_s = c["ms"] / c["n"] / 1e3
-        name, cls = kernel_name(engine, op, tile, fused)
+        name, cls = kernel_name(engine, op, tile, fused, seq)
         n_out = {"qkv": 1152, "ffn1_gelu": 1536}.get(op, 384)
         grid = gemm_grid_items(engine.gemm_tile_name(tile), m, n_out) if tile >= 0 else None
         rows.append({"kernel": name, "class": cls, "op": op, "m": m, "grid_items": grid,
@@ -309,6 +317,9 @@ def short_kernel(name):
     m = re.search(r"gemm_wres_kernel(?:<|ILi)(\d)", n)
     if m:
         return f"gemm_wres_kernel<{m.group(1)}>"
+    m = re.search(r"qkv_attention_kernel(?:<|ILi)(\d+)", n)
+    if m:
+        return f"qkv_attention_kernel<{m.group(1)}>"
     m = (re.search(r"attention_kernel<(\d+),(\d+),(\d+),(\w+)>", n) or
          re.search(r"attention_kernelILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)E", n))
     if m:

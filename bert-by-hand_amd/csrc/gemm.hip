@@ -1178,18 +1178,21 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
           (__attribute__((address_space(3))) void*)(dst + sl * 2048 + (g & 3) * 512), 16, 0, 0);
     }
   };
-  // LayerNorm: tile i's residual rows (rows past M read row M - 1) into LDS,
-  // two 1 KB copies per wavefront; LDS chunk slot c of row r holds logical
-  // chunk (c & ~7) | ((c ^ r) & 7).
+  // LayerNorm: tile i's residual rows (rows past M read row M - 1) into LDS.
+  // Each wavefront copies exactly the part it reads back, its own 32
+  // columns (16-byte chunks 4 wave .. 4 wave + 3) of the 32 rows, so that it
+  // waits for its own copies only, with no barrier: copy j2 (1 KB) holds rows
+  // 16 j2 .. +15, lane l row 16 j2 + l / 4 in slot l % 4, which holds
+  // logical chunk (l % 4) ^ ((row >> 2) & 3) (the 16 rows of one read fall on
+  // distinct banks).
   auto issue_res = [&](int i) {
     const int t = mg + i * groups;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int q = (j * NW + wave) * 64 + lane, r = q / (K / 8), c = q % (K / 8);
-      const int cl = (c & ~7) | ((c ^ r) & 7);
+    for (int j2 = 0; j2 < 2; ++j2) {
+      const int r = 16 * j2 + (lane >> 2), c = 4 * wave + ((lane & 3) ^ ((r >> 2) & 3));
       __builtin_amdgcn_global_load_lds(
-          residual + (size_t)min(t * BM + r, M - 1) * K + cl * 8,
-          (__attribute__((address_space(3))) void*)(resid + (j * NW + wave) * 512), 16, 0, 0);
+          residual + (size_t)min(t * BM + r, M - 1) * K + c * 8,
+          (__attribute__((address_space(3))) void*)(resid + (j2 * NW + wave) * 512), 16, 0, 0);
     }
   };
 #pragma unroll
@@ -1235,52 +1238,54 @@ __global__ __launch_bounds__(wres::THREADS) void gemm_wres_kernel(
     f16* stg = smem + RING * TILE + wave * 32 * kStageLd;
     if constexpr (EPI == kLayerNorm) {
       // N = 384: the workgroup owns whole rows.  v = acc + bias + residual,
-      // then two-pass row statistics: per-lane sums over 16 columns, lane ^ 32
-      // holds the wavefront's other 16, LDS across the 12 wavefronts.  A
-      // wavefront reads only the residual elements it then overwrites, so
-      // out may alias residual.
-      float* red = reinterpret_cast<float*>(smem + RING * TILE + NW * 32 * kStageLd);  // [2][NW][32]
-      // The residual copies of this tile: only those of tile i+RING-1 were
-      // issued after them.
+      // then the row statistics in one exchange: each wavefront's mean and
+      // squared deviation over its 32 columns (a lane's 16, lane ^ 32 holds
+      // the other 16), combined across the 12 wavefronts as equal-size
+      // groups (Chan et al.).  A wavefront reads only the residual elements
+      // it then overwrites, so out may alias residual.
+      float2* red = reinterpret_cast<float2*>(smem + RING * TILE + NW * 32 * kStageLd);  // [NW][32]
+      // This wavefront's residual copies of the tile: only those of tile
+      // i+RING-1 were issued after them.
       if (i + RING - 1 < my)
         wait_vm<CPW>();
       else
         wait_vm<0>();
-      lds_barrier();  // every wavefront's residual copies visible
       const f16* cv = colv + wave * 32 + 4 * kh;
 #pragma unroll
       for (int j = 0; j < 4; ++j) bq[j] = *reinterpret_cast<const f16x4*>(cv + 8 * j);
+      const f16* rrow = resid + ((r32 >> 4) * NW + wave) * 512 + (r32 & 15) * 32 + 4 * kh;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = wave * 4 + j;  // logical 16-byte chunk of the row: columns 8c .. 8c+7
-        const f16x4 rv = *reinterpret_cast<const f16x4*>(
-            resid + r32 * K + (((c & ~7) | ((c ^ r32) & 7)) << 3) + 4 * kh);
+      for (int j = 0; j < 4; ++j) {  // columns wave * 32 + 8 j + 4 kh .. +3
+        const f16x4 rv = *reinterpret_cast<const f16x4*>(rrow + ((j ^ ((r32 >> 2) & 3)) << 3));
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[4 * j + e] += (float)bq[j][e] + (float)rv[e];
       }
       float sm = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm += acc[e];
-      sm = xor32_sum(sm);
-      if (kh == 0) red[wave * 32 + r32] = sm;
-      lds_barrier();
-      float t = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) t += red[w * 32 + r32];
-      const float mean = t * (1.0f / kHidden);
+      const float mw = xor32_sum(sm) * (1.0f / 32);
       float q = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float d = acc[e] - mean;
+        const float d = acc[e] - mw;
         q += d * d;
       }
       q = xor32_sum(q);
-      if (kh == 0) red[(NW + wave) * 32 + r32] = q;
+      if (kh == 0) red[wave * 32 + r32] = make_float2(mw, q);
       lds_barrier();
-      float t2 = 0.f;
+      float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) t2 += red[(NW + w) * 32 + r32];
-      const float rstd = rsqrtf(t2 * (1.0f / kHidden) + eps);
+      for (int w = 0; w < NW; ++w) t += red[w * 32 + r32].x;
+      const float mean = t * (1.0f / NW);
+      float t2 = 0.f, dd = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {  // read again: registers are short here
+        const float2 pw = red[w * 32 + r32];
+        const float d = pw.x - mean;
+        t2 += pw.y;
+        dd += d * d;
+      }
+      const float rstd = rsqrtf(fmaf(32.f, dd, t2) * (1.0f / kHidden) + eps);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f16x4 g = *reinterpret_cast<const f16x4*>(cv + COLS + 8 * j);

@@ -38,8 +38,8 @@
 // Arithmetic: FFN1's k order, bias add, GELU polynomial and fp16 rounding are
 // those of the GEMM kernels' GELU epilogue; FFN2 accumulates k in their K
 // loop's order; bias + residual and the LayerNorm statistics follow the
-// N = 384 LayerNorm tiles (row sums in four groups of 96 columns, added in
-// order).  Measured against FFN1 and then FFN2 + residual + LayerNorm of the
+// N = 384 LayerNorm tiles (mean and squared deviation per group of 96
+// columns, the four groups combined in order).  Measured against FFN1 and then FFN2 + residual + LayerNorm of the
 // GEMM kernels: equal except on fp16 rounding midpoints (48 of 6.4M outputs at
 // 16592 rows, one fp16 step apart, each kernel as often the nearer to a
 // float64 evaluation).
@@ -216,8 +216,8 @@ __global__ __launch_bounds__(ffnf::THREADS) void ffn_fused_kernel(
             (16 * q * kFfn + IC * c) * 2, 0, 0);
     }
   };
-  // Phase k ends a block (the consumers' epilogue, with three extra
-  // barriers for the LayerNorm partials) when chunk k - 1 is a block's last.
+  // Phase k ends a block (the consumers' epilogue, with two extra barriers
+  // for the LayerNorm partials) when chunk k - 1 is a block's last.
   auto epilogue_phase = [&](int k) { return k >= 1 && (k - 1) % NC == NC - 1; };
 
   // Prologue: pieces 0 (phase 0), 1 and 2 (phase 1); phase 0 waits for piece 0.
@@ -259,8 +259,7 @@ __global__ __launch_bounds__(ffnf::THREADS) void ffn_fused_kernel(
 #pragma unroll
         for (int t = 0; t < KS2; ++t) *reinterpret_cast<f16x8*>(hb + t * 512) = hf[t];
       }
-      if (epilogue_phase(k)) {
-        lds_barrier();
+      if (epilogue_phase(k)) {  // the consumers' two LayerNorm barriers
         lds_barrier();
         lds_barrier();
       }
@@ -308,50 +307,55 @@ __global__ __launch_bounds__(ffnf::THREADS) void ffn_fused_kernel(
             // One block's loads in flight at a time: registers are short here.
             if (jj == 3) __builtin_amdgcn_sched_barrier(0);
           }
-        // Row statistics in the N = 384 LayerNorm tiles' order: per 96-column
-        // group g (this consumer holds groups 2 half, 2 half + 1) a lane's
-        // sum over its 48 values plus lane ^ 32's; the four groups added in
-        // order.  The partials pass through the H buffer that phase k - 1
-        // filled (free once every consumer has read it: first barrier).
-        float* red = reinterpret_cast<float*>(hbuf + ((k - 1) & 1) * HBUF) + strip * 256;
-        float sg[2];
+        // Row statistics as the N = 384 LayerNorm tiles take them: per
+        // 96-column group g (this consumer holds groups 2 half, 2 half + 1)
+        // the mean and squared deviation over a lane's 48 values plus lane ^
+        // 32's, then the four groups combined in order as equal-size groups
+        // (Chan et al.).  The pairs pass through the H buffer that phase
+        // k - 1 filled (free once every consumer has read it: first barrier).
+        float2* red = reinterpret_cast<float2*>(hbuf + ((k - 1) & 1) * HBUF) + strip * 128;
+        float mw[2], qw[2];
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg) {
-          sg[gg] = 0.f;
+          float sg = 0.f;
 #pragma unroll
           for (int b = 3 * gg; b < 3 * gg + 3; ++b)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sg[gg] += y[b][i];
-          sg[gg] = xor32_sum(sg[gg]);
-        }
-        lds_barrier();
-        if (kh == 0) {
-          red[(2 * half) * 32 + r32] = sg[0];
-          red[(2 * half + 1) * 32 + r32] = sg[1];
-        }
-        lds_barrier();
-        float tsum = 0.f;
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) tsum += red[g4 * 32 + r32];
-        const float mean = tsum * (1.0f / kHidden);
-#pragma unroll
-        for (int gg = 0; gg < 2; ++gg) {
+            for (int i = 0; i < 16; ++i) sg += y[b][i];
+          mw[gg] = xor32_sum(sg) * (1.0f / 96);
           float qg = 0.f;
 #pragma unroll
           for (int b = 3 * gg; b < 3 * gg + 3; ++b)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-              y[b][i] -= mean;  // kept centred: the output pass reuses the difference
-              qg += y[b][i] * y[b][i];
+              const float d = y[b][i] - mw[gg];
+              qg += d * d;
             }
-          qg = xor32_sum(qg);
-          if (kh == 0) red[128 + (2 * half + gg) * 32 + r32] = qg;
+          qw[gg] = xor32_sum(qg);
         }
         lds_barrier();
-        float tq = 0.f;
+        if (kh == 0) {
+          red[(2 * half) * 32 + r32] = make_float2(mw[0], qw[0]);
+          red[(2 * half + 1) * 32 + r32] = make_float2(mw[1], qw[1]);
+        }
+        lds_barrier();
+        float tsum = 0.f;
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) tq += red[128 + g4 * 32 + r32];
-        const float rstd = rsqrtf(tq * (1.0f / kHidden) + eps);
+        for (int g4 = 0; g4 < 4; ++g4) tsum += red[g4 * 32 + r32].x;
+        const float mean = tsum * (1.0f / 4);
+        float tq = 0.f, dd = 0.f;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const float2 pw = red[g4 * 32 + r32];
+          const float d = pw.x - mean;
+          tq += pw.y;
+          dd += d * d;
+        }
+        const float rstd = rsqrtf(fmaf(96.f, dd, tq) * (1.0f / kHidden) + eps);
+#pragma unroll
+        for (int b = 0; b < YB; ++b)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) y[b][i] -= mean;  // as the tiles: (v - mean) * rstd * g + b
 #pragma unroll
         for (int b = 0; b < YB; ++b)
 #pragma unroll

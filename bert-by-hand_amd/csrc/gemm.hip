@@ -673,8 +673,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
 
   if constexpr (EPI == kLayerNorm) {
     static_assert(C::BN == kHidden, "LayerNorm tile owns whole 384-wide rows");
-    // v = acc + bias + residual, then two-pass row statistics: per-lane sums,
-    // lane ^ 32 holds the other half of the wave's columns, LDS across wn.
+    // v = acc + bias + residual, then the row statistics (lane ^ 32 holds the
+    // other half of the wave's columns, LDS across wn).
     // The residual rows arrive through the (still free) output staging area:
     // coalesced 16-byte loads, then each lane reads its 4-column runs from
     // LDS.  Tiles staged in passes read their runs from global memory.
@@ -720,6 +720,10 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
         }
       }
     }
+    // Row statistics in one exchange: each wavefront's mean and squared
+    // deviation over its TN columns of the row, combined across the WN
+    // wavefronts of the row as equal-size groups (Chan et al.).
+    float2* red2 = reinterpret_cast<float2*>(red);  // [WN][BM]
 #pragma unroll
     for (int fm = 0; fm < C::FM; ++fm) {
       float s = 0.f;
@@ -727,27 +731,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       for (int fn = 0; fn < C::FN; ++fn)
 #pragma unroll
         for (int i = 0; i < 16; ++i) s += acc[fm][fn][i];
-      s = xor32_sum(s);
-      if (kh == 0) red[wn * C::BM + wm * C::TM + fm * 32 + r32] = s;
-    }
-    lds_barrier();
-#pragma unroll
-    for (int fm = 0; fm < C::FM; ++fm) {
-      const int row = wm * C::TM + fm * 32 + r32;
-      float t = 0.f;
-#pragma unroll
-      for (int w = 0; w < C::WN; ++w) t += red[w * C::BM + row];
-      mean[fm] = t * (1.0f / kHidden);
+      const float mw = xor32_sum(s) * (1.0f / C::TN);
       float q = 0.f;
 #pragma unroll
       for (int fn = 0; fn < C::FN; ++fn)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float d = acc[fm][fn][i] - mean[fm];
+          const float d = acc[fm][fn][i] - mw;
           q += d * d;
         }
       q = xor32_sum(q);
-      if (kh == 0) red[(C::WN + wn) * C::BM + row] = q;
+      if (kh == 0) red2[wn * C::BM + wm * C::TM + fm * 32 + r32] = make_float2(mw, q);
     }
     lds_barrier();
 #pragma unroll
@@ -755,8 +749,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(
       const int row = wm * C::TM + fm * 32 + r32;
       float t = 0.f;
 #pragma unroll
-      for (int w = 0; w < C::WN; ++w) t += red[(C::WN + w) * C::BM + row];
-      rstd[fm] = rsqrtf(t * (1.0f / kHidden) + eps);
+      for (int w = 0; w < C::WN; ++w) t += red2[w * C::BM + row].x;
+      mean[fm] = t * (1.0f / C::WN);
+      float t2 = 0.f, dd = 0.f;
+#pragma unroll
+      for (int w = 0; w < C::WN; ++w) {
+        const float2 pw = red2[w * C::BM + row];
+        const float d = pw.x - mean[fm];
+        t2 += pw.y;
+        dd += d * d;
+      }
+      rstd[fm] = rsqrtf(fmaf((float)C::TN, dd, t2) * (1.0f / kHidden) + eps);
     }
   }
 

@@ -836,7 +836,9 @@ constexpr float kLazy = 8.f;  // as attention_kernel: the running max may lag by
 // A workgroup of BM / 32 wavefronts over BM rows (128, or 192 where a
 // sentence length fills it better).  LDS after the K loop (bytes): Q
 // [BM][32], K [KR][32] (swizzled), V^T [32][VLD], key bias [G][round32(seq)]
-// (at most 2 BM), row (mean, rstd) [BM], fs / fc [2][96].
+// (at most 2 BM), row (mean, rstd) [BM], fs / fc [2][96], and each
+// wavefront's 32 x 32 output tile [32][kOutLd] (all within the K loop's ring).
+constexpr int kOutLd = 40;  // halves per row of a wavefront's output tile
 template <int BM_>
 struct Layout {
   static constexpr int BM = BM_, NWV = BM / 32, NT = 64 * NWV, KR = BM + 32, VLD = KR + 8;
@@ -845,7 +847,8 @@ struct Layout {
   static constexpr size_t OFF_Q = 0, OFF_K = OFF_Q + (size_t)BM * HD * 2,
                           OFF_V = OFF_K + (size_t)KR * HD * 2, OFF_B = OFF_V + (size_t)HD * VLD * 2,
                           OFF_R = OFF_B + (size_t)MBN * 4, OFF_F = OFF_R + (size_t)BM * 8,
-                          END = OFF_F + (size_t)2 * NQ * 4;
+                          OFF_S = (OFF_F + (size_t)2 * NQ * 4 + 15) & ~(size_t)15,
+                          END = OFF_S + (size_t)NWV * 32 * kOutLd * 2;
   static constexpr size_t LDS = C::LDS > END ? C::LDS : END;
   static_assert(OFF_V % 16 == 0 && OFF_R % 16 == 0 && OFF_F % 16 == 0 && (VLD * 2) % 16 == 0,
                 "align");
@@ -968,6 +971,7 @@ __global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
   const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const f16x2 ones = {(f16)1.f, (f16)1.f};
   const float lag = kLazy / c;
+  f16* st = reinterpret_cast<f16*>(lds + L::OFF_S) + wave * 32 * kOutLd;
   for (int qt = wave; qt < gv * ntq; qt += L::NWV) {
     const int g = qt / ntq, t = qt - g * ntq, kb = g * seq;
     // Rows past the sentence read its last row (as attention_kernel clamps
@@ -1031,16 +1035,21 @@ __global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
     }
     const float lt = xor32_sum(l);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    const int q = t * 32 + r32;
-    if (q < seq) {  // o[i] = O[q][8*(i/4) + 4*kh + i%4]
-      f16* dst = ctx + (size_t)(m0 + kb + q) * kHidden + h * HD + 4 * kh;
+    // Out through this wavefront's own LDS tile (o[i] = O[t*32 + r32][8*(i/4)
+    // + 4*kh + i%4]), so that each store writes 16 query rows x 64 contiguous
+    // bytes; the wavefront's LDS accesses stay in order, so no barrier.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f16x4 w;
+    for (int j = 0; j < 4; ++j) {
+      f16x4 w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
-        *reinterpret_cast<f16x4*>(dst + 8 * j) = w;
-      }
+      for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
+      *reinterpret_cast<f16x4*>(st + r32 * kOutLd + 8 * j + 4 * kh) = w;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int row = 16 * p + (lane >> 2), cc = lane & 3, q = t * 32 + row;
+      const f16x8 w = *reinterpret_cast<const f16x8*>(st + row * kOutLd + 8 * cc);
+      if (q < seq) *reinterpret_cast<f16x8*>(ctx + (size_t)(m0 + kb + q) * kHidden + h * HD + 8 * cc) = w;
     }
   }
 }

@@ -34,6 +34,8 @@
 // (folds the reference's separate launch_layernorm(x, ..., residual),
 // src/model/encoder.cu:47-50,61-64, src/kernels/layernorm.cu:17-59).
 
+#include <type_traits>
+
 #include "kernels.h"
 #include "pipe.h"
 
@@ -965,23 +967,36 @@ __global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
   }
   lds_barrier();
 
-  // Attention: query tile t of sentence g (rows g*seq + t*32 ..) per
-  // wavefront, over the sentence's key chunks.
+  // Attention: query tiles t0 .. t0 + T - 1 of sentence g (rows g*seq +
+  // t*32 ..) per wavefront, over the sentence's key chunks.  T = 2 shares
+  // each K and V^T operand read between a sentence's two tiles; each tile
+  // keeps its own rescale decisions, so its bits are those of T = 1.
   const int krow = key_of_row(r32);
   const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const f16x2 ones = {(f16)1.f, (f16)1.f};
   const float lag = kLazy / c;
   f16* st = reinterpret_cast<f16*>(lds + L::OFF_S) + wave * 32 * kOutLd;
-  for (int qt = wave; qt < gv * ntq; qt += L::NWV) {
-    const int g = qt / ntq, t = qt - g * ntq, kb = g * seq;
-    // Rows past the sentence read its last row (as attention_kernel clamps
-    // them), so they take the same rescale decisions; they are not stored.
-    const int qr = kb + min(t * 32 + r32, seq - 1);
-    const f16x8 q0 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 8 * kh);
-    const f16x8 q1 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 16 + 8 * kh);
+  auto attend = [&](auto Tc, int g, int t0) {
+    constexpr int T = decltype(Tc)::value;
+    const int kb = g * seq;
+    f16x8 q0[T], q1[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      // Rows past the sentence read its last row (as attention_kernel clamps
+      // them), so they take the same rescale decisions; they are not stored.
+      const int qr = kb + min((t0 + t) * 32 + r32, seq - 1);
+      q0[t] = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 8 * kh);
+      q1[t] = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 16 + 8 * kh);
+    }
     const float* mbg = mb + g * KP;
-    f32x16 o = zero;
-    float m = 0.f, l = 0.f;
+    f32x16 o[T];
+    float m[T], l[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      o[t] = zero;
+      m[t] = 0.f;
+      l[t] = 0.f;
+    }
     bool started = false;
     for (int kc = 0; kc < ntq; ++kc) {
       const uint32_t bits = (uint32_t)__ballot(mbg[kc * 32 + r32] == 0.f);
@@ -989,68 +1004,102 @@ __global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
       const int key = kb + kc * 32 + krow;
       const f16x8 k0 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, kh));
       const f16x8 k1 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, 2 + kh));
-      f32x16 sc = mfma32(k0, q0, zero);
-      sc = mfma32(k1, q1, sc);  // sc[i]: key kc*32 + 16*(i/8) + 8*kh + i%8 (raw)
+      f32x16 sc[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        sc[t] = mfma32(k0, q0[t], zero);
+        sc[t] = mfma32(k1, q1[t], sc[t]);  // sc[i]: key kc*32 + 16*(i/8) + 8*kh + i%8 (raw)
+      }
       if (bits != 0xffffffffu) {
         const float* mk = mbg + kc * 32 + 8 * kh;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sc[i] += mk[16 * (i >> 3) + (i & 7)];
-      }
-      float v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[0], sc[1]), sc[2]);
+        for (int i = 0; i < 16; ++i) {
+          const float bias = mk[16 * (i >> 3) + (i & 7)];
 #pragma unroll
-      for (int i = 3; i < 15; i += 2)
-        v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(v, sc[i]), sc[i + 1]);
-      v = __builtin_elementwise_maximum(v, sc[15]);
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
-                                                       false, false);
-      const float mx = __builtin_elementwise_maximum(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      const bool up = mx > m + lag;
+          for (int t = 0; t < T; ++t) sc[t][i] += bias;
+        }
+      }
+      float mx[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        float v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[t][0], sc[t][1]),
+                                                sc[t][2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2)
+          v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(v, sc[t][i]), sc[t][i + 1]);
+        v = __builtin_elementwise_maximum(v, sc[t][15]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                         false, false);
+        mx[t] = __builtin_elementwise_maximum(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
       if (!started) {
-        m = mx;
+#pragma unroll
+        for (int t = 0; t < T; ++t) m[t] = mx[t];
         started = true;
-      } else if (__ballot(up)) {
-        const float mn = fmaxf(m, mx);
-        const float corr = __builtin_amdgcn_exp2f((m - mn) * c);
-        l *= corr;
-        o *= corr;
-        m = mn;
+      } else {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          if (__ballot(mx[t] > m[t] + lag)) {
+            const float mn = fmaxf(m[t], mx[t]);
+            const float corr = __builtin_amdgcn_exp2f((m[t] - mn) * c);
+            l[t] *= corr;
+            o[t] *= corr;
+            m[t] = mn;
+          }
       }
       const f16* vrow = Vt + r32 * VLD + kb + kc * 32 + 8 * kh;
       const f16x8 va = *reinterpret_cast<const f16x8*>(vrow);
       const f16x8 vb = *reinterpret_cast<const f16x8*>(vrow + 16);
-      const float mc = m * c;
-      f16x8 pa, pb;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pa[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[i], c, -mc));
-        pb[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[8 + i], c, -mc));
+      for (int t = 0; t < T; ++t) {
+        const float mc = m[t] * c;
+        f16x8 pa, pb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pa[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[t][i], c, -mc));
+          pb[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[t][8 + i], c, -mc));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+          l[t] = __builtin_amdgcn_fdot2(f16x2{pa[i], pa[i + 1]}, ones, l[t], false);
+          l[t] = __builtin_amdgcn_fdot2(f16x2{pb[i], pb[i + 1]}, ones, l[t], false);
+        }
+        o[t] = mfma32(va, pa, o[t]);
+        o[t] = mfma32(vb, pb, o[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float lt = xor32_sum(l[t]);
+      const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+      // Out through this wavefront's own LDS tile (o[i] = O[tile row r32]
+      // [8*(i/4) + 4*kh + i%4]), so that each store writes 16 query rows x 64
+      // contiguous bytes; the wavefront's LDS accesses stay in order, so no
+      // barrier (also between its tiles).
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[t][4 * j + e] * inv);
+        *reinterpret_cast<f16x4*>(st + r32 * kOutLd + 8 * j + 4 * kh) = w;
       }
 #pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        l = __builtin_amdgcn_fdot2(f16x2{pa[i], pa[i + 1]}, ones, l, false);
-        l = __builtin_amdgcn_fdot2(f16x2{pb[i], pb[i + 1]}, ones, l, false);
+      for (int p = 0; p < 2; ++p) {
+        const int row = 16 * p + (lane >> 2), cc = lane & 3, q = (t0 + t) * 32 + row;
+        const f16x8 w = *reinterpret_cast<const f16x8*>(st + row * kOutLd + 8 * cc);
+        if (q < seq)
+          *reinterpret_cast<f16x8*>(ctx + (size_t)(m0 + kb + q) * kHidden + h * HD + 8 * cc) = w;
       }
-      o = mfma32(va, pa, o);
-      o = mfma32(vb, pb, o);
     }
-    const float lt = xor32_sum(l);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    // Out through this wavefront's own LDS tile (o[i] = O[t*32 + r32][8*(i/4)
-    // + 4*kh + i%4]), so that each store writes 16 query rows x 64 contiguous
-    // bytes; the wavefront's LDS accesses stay in order, so no barrier.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f16x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
-      *reinterpret_cast<f16x4*>(st + r32 * kOutLd + 8 * j + 4 * kh) = w;
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int row = 16 * p + (lane >> 2), cc = lane & 3, q = t * 32 + row;
-      const f16x8 w = *reinterpret_cast<const f16x8*>(st + row * kOutLd + 8 * cc);
-      if (q < seq) *reinterpret_cast<f16x8*>(ctx + (size_t)(m0 + kb + q) * kHidden + h * HD + 8 * cc) = w;
-    }
+  };
+  // Two-tile sentences (seq 33 .. 64) a wavefront each where one tile per
+  // wavefront would take two rounds (seq 48 on 192 rows: 8 tiles, 6
+  // wavefronts); otherwise one tile per wavefront.
+  if (ntq == 2 && 2 * gv > L::NWV) {
+    for (int g = wave; g < gv; g += L::NWV) attend(std::integral_constant<int, 2>{}, g, 0);
+  } else {
+    for (int qt = wave; qt < gv * ntq; qt += L::NWV)
+      attend(std::integral_constant<int, 1>{}, qt / ntq, qt % ntq);
   }
 }
 

@@ -1622,8 +1622,9 @@ const char* tile_name(int id) {
 // sweep on four slots moved O-proj to tile 1 as well and QKV to tile 30 up to
 // 4096 rows: pass 4.144-4.160 -> 4.064-4.095 ms in four interleaved repeats;
 // with QKV inside the attention kernel, O-proj to the 128x128 tile (30):
-// 4.117-4.127 -> 4.092-4.104 ms; FFN2 on tile 1 from 1025 rows as well
-// (3.708 -> 3.668 ms, best of four repeats each; alone it is slower there).
+// 4.117-4.127 -> 4.092-4.104 ms; FFN2 on tile 1 and O-proj on tile 30 from
+// 1025 rows as well (3.708 -> 3.668 ms, then 3.845-3.857 -> 3.828-3.843 ms,
+// four repeats each; alone they are slower there).
 // There the other forwards fill the CUs, and fewer, larger tiles move fewer
 // bytes L2 -> CU per FLOP.
 int pick_plain(int M, int N, int K, bool shared) {
@@ -1632,7 +1633,7 @@ int pick_plain(int M, int N, int K, bool shared) {
   if (M <= 1024)
     id = qkv ? (shared ? 30 : 0) : ffn1 ? 0 : 26;
   else if (M <= 2048)
-    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : (shared && wide_k) ? 1 : 26;
+    id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 26 : wide_k ? 1 : 30;
   else if (M <= 3072)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 34 : wide_k ? 1 : 30;
   else if (M <= 4096)

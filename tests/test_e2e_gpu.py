@@ -398,7 +398,7 @@ def test_embed_each_equals_bert_embed_bitwise(torch_cuda, ws, model):
     # rows still normalised.  Op timing with a slot on the caller's stream:
     # one record per launch, each finished when read.  Pools of several slots
     # pick other GEMM tiles from 1025 to 4096 rows (FFN1 128x128 at M = 2048
-    # and 3072, FFN2 64x128 at 2048 to 4096, O-proj 128x128 at 3072 and 4096) than
+    # and 3072, FFN2 64x128 and O-proj 128x128 at 2048 to 4096) than
     # bert_embed and one slot:
     # the bits do not change.
     from bbh import engine

@@ -1095,7 +1095,72 @@ __global__ __launch_bounds__(2 * BM_) void qkv_attention_kernel(
   // Two-tile sentences (seq 33 .. 64) a wavefront each where one tile per
   // wavefront would take two rounds (seq 48 on 192 rows: 8 tiles, 6
   // wavefronts); otherwise one tile per wavefront.
-  if (ntq == 2 && 2 * gv > L::NWV) {
+  // Seq 16: two sentences a 32-row tile (queries and keys 0-15 of sentence
+  // g0, 16-31 of g0 + 1) with the cross-sentence pairs masked, so half the
+  // tiles.  A query's probabilities and sums are those of its own sentence's
+  // tile: the other sentence's keys give exact zeros in the same MFMA and
+  // fdot2 positions its padding keys held there.
+  if (seq == 16) {
+    for (int pr = wave; 2 * pr < gv; pr += L::NWV) {
+      const int g0 = 2 * pr, kb = g0 * 16, qs = r32 >> 4;  // this lane's query: sentence g0 + qs
+      const int qr = min(kb + r32, R - 1);
+      const f16x8 q0 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 8 * kh);
+      const f16x8 q1 = *reinterpret_cast<const f16x8*>(Qs + qr * HD + 16 + 8 * kh);
+      const int key = kb + krow;
+      const f16x8 k0 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, kh));
+      const f16x8 k1 = *reinterpret_cast<const f16x8*>(Ks + ks_off(key, 2 + kh));
+      f32x16 sc = mfma32(k0, q0, zero);
+      sc = mfma32(k1, q1, sc);  // sc[i]: key 16*(i/8) + 8*kh + i%8 of the tile, sentence g0 + i/8
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int ks = i >> 3;
+        sc[i] += (ks == qs && g0 + ks < gv) ? mb[(g0 + ks) * KP + 8 * kh + (i & 7)] : -INFINITY;
+      }
+      float v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[0], sc[1]), sc[2]);
+#pragma unroll
+      for (int i = 3; i < 15; i += 2)
+        v = __builtin_elementwise_maximum(__builtin_elementwise_maximum(v, sc[i]), sc[i + 1]);
+      v = __builtin_elementwise_maximum(v, sc[15]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                       false, false);
+      const float mx = __builtin_elementwise_maximum(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      // every key of the query's sentence masked: zero context, as a skipped chunk gives
+      const float mc = (mx == -INFINITY ? 0.f : mx) * c;
+      const f16* vrow = Vt + r32 * VLD + kb + 8 * kh;
+      const f16x8 va = *reinterpret_cast<const f16x8*>(vrow);
+      const f16x8 vb = *reinterpret_cast<const f16x8*>(vrow + 16);
+      f16x8 pa, pb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pa[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[i], c, -mc));
+        pb[i] = (f16)__builtin_amdgcn_exp2f(fmaf(sc[8 + i], c, -mc));
+      }
+      float l = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        l = __builtin_amdgcn_fdot2(f16x2{pa[i], pa[i + 1]}, ones, l, false);
+        l = __builtin_amdgcn_fdot2(f16x2{pb[i], pb[i + 1]}, ones, l, false);
+      }
+      f32x16 o = mfma32(va, pa, zero);
+      o = mfma32(vb, pb, o);
+      const float lt = xor32_sum(l);
+      const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (f16)(o[4 * j + e] * inv);
+        *reinterpret_cast<f16x4*>(st + r32 * kOutLd + 8 * j + 4 * kh) = w;
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int row = 16 * p + (lane >> 2), cc = lane & 3;
+        const f16x8 w = *reinterpret_cast<const f16x8*>(st + row * kOutLd + 8 * cc);
+        if (kb + row < R)
+          *reinterpret_cast<f16x8*>(ctx + (size_t)(m0 + kb + row) * kHidden + h * HD + 8 * cc) = w;
+      }
+    }
+  } else if (ntq == 2 && 2 * gv > L::NWV) {
     for (int g = wave; g < gv; g += L::NWV) attend(std::integral_constant<int, 2>{}, g, 0);
   } else {
     for (int qt = wave; qt < gv * ntq; qt += L::NWV)

@@ -327,13 +327,15 @@ def test_qkv_attention_kernel_equals_two_kernels(torch_cuda, ws, model):
     # 80 and 96 (192-row workgroups of two sentences, as for seq 48), 112
     # (one sentence a 128-row workgroup, 16 rows idle), and batch sizes that
     # leave the last sentence group of a workgroup part-filled (48 x 5: four
-    # sentences, then one; 32 x 3; 64 x 3).
+    # sentences, then one; 32 x 3; 64 x 3; 16 x 13: eight, then five, so
+    # the last two-sentence tile holds one).
     from bbh import engine, synth
 
     torch = torch_cuda
     batches = synth.varlen_mix()[:12]
     rng = np.random.default_rng(41)
-    for S, B in ((128, 24), (16, 40), (80, 9), (96, 7), (112, 2), (48, 5), (32, 3), (64, 3)):
+    for S, B in ((128, 24), (16, 40), (16, 13), (80, 9), (96, 7), (112, 2), (48, 5), (32, 3),
+                 (64, 3)):
         n = rng.integers(1, S + 1, size=B)
         mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
         ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)

@@ -1677,7 +1677,8 @@ const char* tile_name(int id) {
 // and FFN2 from 2049 rows run the 64x64 copy ring with two K slices per
 // barrier (34; one-slot varlen pass 9.00-9.03 -> 8.84-8.95 ms).  More
 // workgroups than CUs keep every CU busy, and the deeper rings fit beside
-// nothing else.
+// nothing else.  At 513-1024 rows alone FFN1 takes tile 34 (configs[1]
+// forward 195.4-195.8 -> 194.6-194.8 us, four interleaved repeats).
 // Beside other forwards (shared true: a pool of several slots) every tile was
 // tried for each (shape, M) with the others fixed in the per-batch pass, then
 // the winners confirmed in interleaved repeats: FFN1 takes the 128x128
@@ -1696,7 +1697,7 @@ int pick_plain(int M, int N, int K, bool shared) {
   const bool qkv = N == 1152, ffn1 = N == 1536, wide_k = K >= 1024;
   int id;
   if (M <= 1024)
-    id = qkv ? (shared ? 30 : 0) : ffn1 ? 0 : 26;
+    id = qkv ? (shared ? 30 : 0) : ffn1 ? (!shared && M > 512 ? 34 : 0) : 26;
   else if (M <= 2048)
     id = qkv ? 30 : ffn1 ? (shared ? 30 : 0) : !shared ? 26 : wide_k ? 1 : 30;
   else if (M <= 3072)

@@ -1678,7 +1678,10 @@ const char* tile_name(int id) {
 // barrier (34; one-slot varlen pass 9.00-9.03 -> 8.84-8.95 ms).  More
 // workgroups than CUs keep every CU busy, and the deeper rings fit beside
 // nothing else.  At 513-1024 rows alone FFN1 takes tile 34 (configs[1]
-// forward 195.4-195.8 -> 194.6-194.8 us, four interleaved repeats).
+// forward 195.4-195.8 -> 194.6-194.8 us, four interleaved repeats); at
+// 6145-8192 rows alone FFN1 takes tile 31, FFN2 tile 30 and O-proj tile 0
+// (configs[2] forward 387.5 -> 383.5 us on one box, every repeat; level on
+// a slower one).
 // Beside other forwards (shared true: a pool of several slots) every tile was
 // tried for each (shape, M) with the others fixed in the per-batch pass, then
 // the winners confirmed in interleaved repeats: FFN1 takes the 128x128
@@ -1707,7 +1710,7 @@ int pick_plain(int M, int N, int K, bool shared) {
   else if (M <= 6144)
     id = qkv ? 30 : ffn1 ? 26 : wide_k ? 31 : 0;
   else if (M <= 8192)
-    id = wide_k ? 31 : 30;
+    id = shared ? (wide_k ? 31 : 30) : qkv ? 30 : ffn1 ? 31 : wide_k ? 30 : 0;
   else if (M <= 16384)
     id = wide_k ? 32 : 30;
   else if (M <= 49152)

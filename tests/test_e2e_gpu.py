@@ -328,7 +328,8 @@ def test_qkv_attention_kernel_equals_two_kernels(torch_cuda, ws, model):
     # (one sentence a 128-row workgroup, 16 rows idle), and batch sizes that
     # leave the last sentence group of a workgroup part-filled (48 x 5: four
     # sentences, then one; 32 x 3; 64 x 3; 16 x 13: eight, then five, so
-    # the last two-sentence tile holds one).
+    # the last two-sentence tile holds one, and an empty sentence beside a
+    # full one in a tile).
     from bbh import engine, synth
 
     torch = torch_cuda
@@ -337,6 +338,8 @@ def test_qkv_attention_kernel_equals_two_kernels(torch_cuda, ws, model):
     for S, B in ((128, 24), (16, 40), (16, 13), (80, 9), (96, 7), (112, 2), (48, 5), (32, 3),
                  (64, 3)):
         n = rng.integers(1, S + 1, size=B)
+        if (S, B) == (16, 13):
+            n[3] = 0  # an empty sentence sharing a two-sentence tile with a full one
         mask = (np.arange(S)[None, :] < n[:, None]).astype(np.int32)
         ids = (rng.integers(1000, 30522, size=(B, S)) * mask).astype(np.int32)
         batches.append((ids, np.zeros_like(ids), mask, S))
